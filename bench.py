@@ -1,0 +1,146 @@
+#!/usr/bin/env python3
+"""Headline benchmark: effective INT8 TOPS of the dispatched kernel on the
+BASELINE configuration 2 layer (N=32, 28x28, C=K=128, 3x3, stride 1, pad 1;
+the layer the >=50%-of-peak target is quoted on), on one GPU.
+
+A step = one convolution of the whole layer (7.40 GOP) with input, filter,
+bias and output resident in HBM.  Before timing, the GPU output is checked
+bit-exact against the CPU oracle (the reference's check-before-time
+contract, conv_lab.cu:193-194).  Timing: W warmup launches, synchronize,
+then exactly K back-to-back launches between one pair of HIP events on the
+launch stream (plus the reference's per-launch median, conv_lab.cu:88-110).
+
+Prints one JSON line.  --gpus N > 1 is not supported (one GPU per box).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA, published
+PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E, published
+WORKLOAD = "cfg2_resnet_3x3_s1"
+
+
+def cpu_baseline(shape, x, w, b, threads: int, min_cpu_seconds: float = 10.0):
+    """The oracle (a port of conv_lab.cu:39-66) on the host cores, repeated
+    over the full layer until about `min_cpu_seconds` of CPU work."""
+    from oracle import oracle
+    reps, t_total = 0, 0.0
+    while True:
+        t0 = time.perf_counter()
+        oracle.conv(shape, x, w, b, threads=threads)
+        t_total += time.perf_counter() - t0
+        reps += 1
+        if t_total * threads >= min_cpu_seconds or reps >= 50:
+            break
+    tops = shape.ops() * reps / t_total / 1e12
+    return {"value": round(tops, 6), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"oracle.conv over the full {WORKLOAD} layer x{reps} "
+                      f"({reps * shape.ops() / 1e9:.1f} GOP, {t_total:.2f} s wall)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--kernel", default="dispatch",
+                    help="dispatch (default) or one of generic|strip|halo|splitk")
+    ap.add_argument("--workload", default=WORKLOAD)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this lab measures one GPU "
+              "(each box has one MI355X; the layer is not sharded across GPUs)", file=sys.stderr)
+        return 2
+    if args.steps <= 0 or args.warmup < 0:
+        print("bench.py: --steps must be > 0 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import int8_kernel_lab_amd as lab
+    from oracle import oracle
+
+    shape = lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), args.workload)
+    kernel = lab.dispatch(shape) if args.kernel == "dispatch" else args.kernel
+    g = shape.geometry()
+    x, w, b = lab.make_case_data(shape)
+    xb, wb, bb = (lab.DeviceBuffer.from_array(a) for a in (x, w, b))
+    yb = lab.DeviceBuffer(4 * g.output_elements)
+    ws_n = lab.workspace_bytes(kernel, shape)
+    ws = lab.DeviceBuffer(ws_n) if ws_n else None
+
+    # correctness before timing: full output vs the CPU oracle
+    yb.fill(0xA5)
+    lab.launch(kernel, shape, xb, wb, bb, yb, ws, ws_n)
+    lab.synchronize()
+    got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
+    expected = oracle.conv(shape, x, w, b)
+    if not np.array_equal(got, expected):
+        print(f"bench.py: {kernel} output differs from the oracle on {args.workload}",
+              file=sys.stderr)
+        return 1
+
+    median_ms, mean_ms = lab.measure(kernel, shape, xb, wb, bb, yb, ws, ws_n,
+                                     warmup=args.warmup, iterations=args.steps)
+    ops = shape.ops()
+    nbytes = shape.algorithmic_bytes()
+    tops = ops / (mean_ms * 1e-3) / 1e12
+    gbps = nbytes / (mean_ms * 1e-3) / 1e9
+    info = lab.device_info()
+    threads = min(16, os.cpu_count() or 1)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(shape, x, w, b, threads)
+
+    line = {
+        "metric": "effective INT8 TOPS per conv layer + % of MI355X dense INT8 MFMA peak",
+        "value": round(tops, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 (int32 accumulate)",
+        "data": "synthetic (SplitMix64 seed 20260925: int8 U[-128,127], bias U[-2^20,2^20])",
+        "config": {
+            "workload": f"{args.workload}: N={shape.n} H=W={shape.h} C={shape.c} K={shape.k} "
+                        f"{shape.r}x{shape.s} stride {shape.stride_h} pad {shape.pad_h}",
+            "kernel": kernel,
+            "gemm_mnk": [g.gemm_m, g.gemm_n, g.gemm_k],
+            "ops_per_step": ops,
+            "algorithmic_bytes_per_step": nbytes,
+            "pct_int8_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
+            "per_launch_median_ms": round(median_ms, 6),
+            "device": info["arch"],
+            "compute_units": info["compute_units"],
+            "parallelism": "single GPU",
+        },
+        # op/B = 457 < ridge 625 (5.0 POPS / 8 TB/s): HBM is the binding roof
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    for buf in (xb, wb, bb, yb, ws):
+        if buf is not None:
+            buf.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,190 @@
+/*
+ * i8conv.h - C ABI of the MI355X (gfx950) INT8 implicit-GEMM convolution lab.
+ *
+ * Contract (same as the reference's launchers):
+ *   input  x    : NHWC int8          n*h*w*c bytes
+ *   filter w    : KRSC int8          k*r*s*c bytes
+ *   bias   b    : K int32            k values
+ *   output y    : NHWK int32         n*out_h*out_w*k values
+ *   y[m][j] = b[j] + sum over valid taps (fy, fx) and channels ci of
+ *             x[batch][iy][ix][ci] * w[j][fy][fx][ci]      (int32, exact)
+ * Every in-range output element is overwritten (beta = 0).  Taps that fall
+ * outside the image contribute nothing (zero padding).
+ *
+ * Conventions of this ABI:
+ *   - plain C types only; `stream` is a hipStream_t passed as void* (NULL is
+ *     the default stream);
+ *   - device pointers come from the caller (or from i8conv_device_alloc); the
+ *     launch entry points allocate nothing;
+ *   - input and filter base addresses must be 16-byte aligned, output and bias
+ *     4-byte aligned (16-byte for the vector epilogue, checked at launch);
+ *   - every function returns an i8conv_status (never exits the process);
+ *     i8conv_last_error() describes the most recent failure on this thread.
+ *
+ * Reference interfaces replaced (file:line in pthodima/int8_kernel_lab):
+ *   ConvShape<...>                include/conv_shape.cuh:5-36
+ *   launch_generic<Shape>         include/generic_implicit_gemm.cuh:155-165
+ *   launch_generic_sm80<Shape>    include/generic_implicit_gemm.cuh:229-238
+ *   launch_spatial_strip<Shape>   include/spatial_strip.cuh:289-301
+ *   kSpatialStripEligible<Shape>  include/spatial_strip.cuh:11-15
+ *   DeviceBuffer<T>               src/conv_lab.cu:24-37
+ *   measure(launch, warmup, it)   src/conv_lab.cu:88-110
+ * The halo-tiled and split-K entries have no reference counterpart (the
+ * reference names neither); they follow the same launcher contract.
+ */
+#ifndef I8CONV_H
+#define I8CONV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Runtime shape descriptor: the 13 template parameters of ConvShape
+ * (include/conv_shape.cuh:5-21), same names and meaning. */
+typedef struct i8conv_shape {
+  int32_t n, h, w, c, k, r, s;
+  int32_t pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w;
+} i8conv_shape;
+
+/* Derived geometry (include/conv_shape.cuh:22-32). */
+typedef struct i8conv_geometry {
+  int32_t out_h, out_w;
+  int64_t gemm_m; /* n * out_h * out_w */
+  int32_t gemm_n; /* k */
+  int32_t gemm_k; /* r * s * c */
+  int64_t input_elements, filter_elements, output_elements;
+} i8conv_geometry;
+
+typedef enum i8conv_status {
+  I8CONV_OK = 0,
+  I8CONV_INELIGIBLE = 1,       /* kernel's predicate rejects the shape */
+  I8CONV_BAD_SHAPE = 2,        /* shape violates conv_shape.cuh:34-35 or limits */
+  I8CONV_BAD_ARGUMENT = 3,     /* null/misaligned pointer, bad count, ... */
+  I8CONV_WORKSPACE_TOO_SMALL = 4,
+  I8CONV_HIP_ERROR = 5,        /* a HIP runtime call failed */
+  I8CONV_UNKNOWN_KERNEL = 6
+} i8conv_status;
+
+/* Kernel ids of the candidate family. */
+enum {
+  I8CONV_KERNEL_GENERIC = 0, /* staged implicit GEMM, any shape with c%16==0 */
+  I8CONV_KERNEL_STRIP = 1,   /* 3x3 horizontal-stride-1 spatial strip */
+  I8CONV_KERNEL_HALO = 2,    /* 2-D output tile with LDS-resident input halo */
+  I8CONV_KERNEL_SPLITK = 3,  /* split reduction + deterministic second pass */
+  I8CONV_KERNEL_COUNT = 4
+};
+
+/* ---- shape ------------------------------------------------------------- */
+
+/* Fills *geometry.  I8CONV_BAD_SHAPE when c%16 != 0, the output is empty, a
+ * field is out of range (n,h,w,c,k,r,s,stride,dilation >= 1, pad >= 0), or a
+ * tensor exceeds 2^31-1 bytes.  Replaces conv_shape.cuh:22-35. */
+int i8conv_derive(const i8conv_shape *shape, i8conv_geometry *geometry);
+
+/* ---- kernel registry (host only, no GPU needed) ------------------------ */
+
+int i8conv_kernel_count(void);
+/* Name of kernel `id` ("generic", "strip", "halo", "splitk"), NULL if unknown. */
+const char *i8conv_kernel_name(int id);
+/* Id of a kernel by name, or -1. */
+int i8conv_kernel_id(const char *name);
+/* 1 if kernel `id` can run `shape`, else 0 (also 0 for a bad shape or id).
+ * The strip predicate replaces kSpatialStripEligible (spatial_strip.cuh:11-15),
+ * re-derived for the gfx950 tile. */
+int i8conv_eligible(int id, const i8conv_shape *shape);
+/* Device workspace a launch of `id` on `shape` needs, in bytes (0 for all
+ * kernels but split-K).  0 also for an ineligible shape. */
+size_t i8conv_workspace_bytes(int id, const i8conv_shape *shape);
+
+/* ---- dispatch policy (kept outside the kernels) ------------------------ */
+
+/* Kernel id the policy picks for `shape` (always an eligible one), or -1 for
+ * a bad shape.  Implements the "encode the policy outside the kernels" step
+ * of the reference's workflow (README.md:92-99). */
+int i8conv_dispatch(const i8conv_shape *shape);
+/* Workspace the dispatched kernel needs. */
+size_t i8conv_dispatch_workspace_bytes(const i8conv_shape *shape);
+
+/* ---- launch (asynchronous on `stream`) --------------------------------- */
+
+/* Launches kernel `id`.  `workspace` may be NULL when workspace_bytes is 0.
+ * Returns I8CONV_INELIGIBLE for a shape the predicate rejects (the reference
+ * made that a compile error, spatial_strip.cuh:202-203), I8CONV_HIP_ERROR if
+ * the launch fails.  Allocates nothing. */
+int i8conv_launch(int id, const i8conv_shape *shape, const int8_t *input,
+                  const int8_t *filter, const int32_t *bias, int32_t *output,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
+/* launch_generic<Shape> (generic_implicit_gemm.cuh:155-165) and its sm80
+ * twin (:229-238): one gfx950 kernel replaces both. */
+int i8conv_launch_generic(const i8conv_shape *shape, const int8_t *input,
+                          const int8_t *filter, const int32_t *bias,
+                          int32_t *output, void *stream);
+/* launch_spatial_strip<Shape> (spatial_strip.cuh:289-301). */
+int i8conv_launch_spatial_strip(const i8conv_shape *shape, const int8_t *input,
+                                const int8_t *filter, const int32_t *bias,
+                                int32_t *output, void *stream);
+/* kSpatialStripEligible<Shape> (spatial_strip.cuh:11-15), re-derived. */
+int i8conv_spatial_strip_eligible(const i8conv_shape *shape);
+/* Launches whatever i8conv_dispatch picks. */
+int i8conv_launch_dispatched(const i8conv_shape *shape, const int8_t *input,
+                             const int8_t *filter, const int32_t *bias,
+                             int32_t *output, void *workspace,
+                             size_t workspace_bytes, void *stream);
+
+/* ---- thin HIP runtime layer used by the host driver -------------------- */
+
+/* DeviceBuffer (conv_lab.cu:24-37) as C calls. */
+int i8conv_device_count(int *count);
+int i8conv_set_device(int device);
+int i8conv_device_alloc(void **ptr, size_t bytes);
+int i8conv_device_free(void *ptr);
+int i8conv_copy_to_device(void *dst, const void *src, size_t bytes);
+int i8conv_copy_to_host(void *dst, const void *src, size_t bytes);
+/* Fills `bytes` of device memory with the byte `value` (poisoning before a
+ * correctness run). */
+int i8conv_device_fill(void *ptr, int value, size_t bytes);
+int i8conv_synchronize(void);
+int i8conv_stream_create(void **stream);
+int i8conv_stream_destroy(void *stream);
+
+/* Device facts for roofline reporting: compute units, peak engine clock in
+ * kHz, gcnArchName (at most `name_len` bytes incl. NUL). */
+int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
+                       size_t name_len);
+
+/* measure() (conv_lab.cu:88-110): `warmup` launches, synchronize, then
+ * `iterations` launches each bracketed by its own event pair on `stream` and
+ * synchronized; *median_ms is the median.  When batched_ms is non-NULL it
+ * also times `iterations` back-to-back launches between one event pair and
+ * stores the mean per launch (exposes per-launch event overhead). */
+int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
+                   const int8_t *filter, const int32_t *bias, int32_t *output,
+                   void *workspace, size_t workspace_bytes, void *stream,
+                   int warmup, int iterations, float *median_ms,
+                   float *batched_ms);
+
+/* ---- errors and synthetic data ----------------------------------------- */
+
+const char *i8conv_status_string(int status);
+/* Text of the most recent failure on the calling thread ("" if none). */
+const char *i8conv_last_error(void);
+
+/* Seeded synthetic data (host memory).  SplitMix64 (Steele, Lea, Flood,
+ * "Fast splittable pseudorandom number generators", OOPSLA 2014) advanced
+ * from `*state`; value i = lo + (next() mod (hi - lo + 1)).  `*state` is
+ * updated so that successive calls continue one stream (input, then filter,
+ * then bias). */
+void i8conv_fill_int8(int8_t *dst, size_t count, int lo, int hi,
+                      uint64_t *state);
+void i8conv_fill_int32(int32_t *dst, size_t count, int32_t lo, int32_t hi,
+                       uint64_t *state);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* I8CONV_H */

@@ -1,0 +1,330 @@
+// The C ABI: registry, eligibility, launch, and the thin HIP runtime layer
+// the host driver uses (allocation, copies, events).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "i8conv_internal.hpp"
+
+namespace i8conv {
+
+namespace {
+thread_local std::string g_last_error;
+
+const char *const kNames[I8CONV_KERNEL_COUNT] = {"generic", "strip", "halo", "splitk"};
+
+int hip_fail(const char *what, hipError_t e) {
+  set_error(std::string(what) + ": " + hipGetErrorString(e));
+  return I8CONV_HIP_ERROR;
+}
+
+bool aligned(const void *p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+}  // namespace
+
+void set_error(const std::string &message) { g_last_error = message; }
+
+}  // namespace i8conv
+
+using namespace i8conv;
+
+extern "C" {
+
+int i8conv_derive(const i8conv_shape *shape, i8conv_geometry *geometry) {
+  if (!shape) {
+    set_error("null shape");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  return derive(*shape, geometry);
+}
+
+int i8conv_kernel_count(void) { return I8CONV_KERNEL_COUNT; }
+
+const char *i8conv_kernel_name(int id) {
+  return (id >= 0 && id < I8CONV_KERNEL_COUNT) ? kNames[id] : nullptr;
+}
+
+int i8conv_kernel_id(const char *name) {
+  if (!name) return -1;
+  for (int i = 0; i < I8CONV_KERNEL_COUNT; ++i)
+    if (std::string(name) == kNames[i]) return i;
+  return -1;
+}
+
+int i8conv_eligible(int id, const i8conv_shape *shape) {
+  if (!shape) return 0;
+  i8conv_geometry g;
+  if (derive(*shape, &g) != I8CONV_OK) return 0;
+  PatchPlan pp;
+  switch (id) {
+    case I8CONV_KERNEL_GENERIC: return 1;
+    case I8CONV_KERNEL_STRIP: return plan_strip(*shape, g, &pp) ? 1 : 0;
+    case I8CONV_KERNEL_HALO: return plan_halo(*shape, g, &pp) ? 1 : 0;
+    case I8CONV_KERNEL_SPLITK: return plan_generic(g).stages >= 2 ? 1 : 0;
+    default: return 0;
+  }
+}
+
+size_t i8conv_workspace_bytes(int id, const i8conv_shape *shape) {
+  if (id != I8CONV_KERNEL_SPLITK || !i8conv_eligible(id, shape)) return 0;
+  i8conv_geometry g;
+  derive(*shape, &g);
+  return splitk_workspace_bytes(g, plan_splitk(g));
+}
+
+int i8conv_dispatch(const i8conv_shape *shape) {
+  if (!shape) return -1;
+  return dispatch(*shape);
+}
+
+size_t i8conv_dispatch_workspace_bytes(const i8conv_shape *shape) {
+  const int id = i8conv_dispatch(shape);
+  return id < 0 ? 0 : i8conv_workspace_bytes(id, shape);
+}
+
+int i8conv_launch(int id, const i8conv_shape *shape, const int8_t *input,
+                  const int8_t *filter, const int32_t *bias, int32_t *output,
+                  void *workspace, size_t workspace_bytes, void *stream) {
+  if (id < 0 || id >= I8CONV_KERNEL_COUNT) {
+    set_error("unknown kernel id " + std::to_string(id));
+    return I8CONV_UNKNOWN_KERNEL;
+  }
+  if (!shape) {
+    set_error("null shape");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  i8conv_geometry g;
+  const int rc = derive(*shape, &g);
+  if (rc != I8CONV_OK) return rc;
+  if (!input || !filter || !bias || !output) {
+    set_error("null tensor pointer");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  if (!aligned(input, 16) || !aligned(filter, 16) || !aligned(bias, 4) ||
+      !aligned(output, 4)) {
+    set_error("input/filter must be 16-byte aligned, bias/output 4-byte aligned");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  const ConvArgs args = make_args(*shape, g, input, filter, bias, output);
+  switch (id) {
+    case I8CONV_KERNEL_GENERIC:
+      return launch_gemm(args, plan_generic(g), stream);
+    case I8CONV_KERNEL_STRIP:
+    case I8CONV_KERNEL_HALO: {
+      PatchPlan pp;
+      const bool ok = id == I8CONV_KERNEL_STRIP ? plan_strip(*shape, g, &pp)
+                                                : plan_halo(*shape, g, &pp);
+      if (!ok) {
+        set_error(std::string(kNames[id]) + " is not eligible for this shape");
+        return I8CONV_INELIGIBLE;
+      }
+      return launch_patch(args, pp, stream);
+    }
+    case I8CONV_KERNEL_SPLITK: {
+      if (!i8conv_eligible(id, shape)) {
+        set_error("splitk needs at least two 128-byte k stages");
+        return I8CONV_INELIGIBLE;
+      }
+      const GemmPlan p = plan_splitk(g);
+      const size_t need = splitk_workspace_bytes(g, p);
+      if (!workspace || workspace_bytes < need || !aligned(workspace, 16)) {
+        set_error("splitk needs a 16-byte aligned workspace of " +
+                  std::to_string(need) + " bytes");
+        return I8CONV_WORKSPACE_TOO_SMALL;
+      }
+      return launch_splitk(args, p, workspace, stream);
+    }
+  }
+  return I8CONV_UNKNOWN_KERNEL;
+}
+
+int i8conv_launch_generic(const i8conv_shape *shape, const int8_t *input,
+                          const int8_t *filter, const int32_t *bias,
+                          int32_t *output, void *stream) {
+  return i8conv_launch(I8CONV_KERNEL_GENERIC, shape, input, filter, bias,
+                       output, nullptr, 0, stream);
+}
+
+int i8conv_launch_spatial_strip(const i8conv_shape *shape, const int8_t *input,
+                                const int8_t *filter, const int32_t *bias,
+                                int32_t *output, void *stream) {
+  return i8conv_launch(I8CONV_KERNEL_STRIP, shape, input, filter, bias, output,
+                       nullptr, 0, stream);
+}
+
+int i8conv_spatial_strip_eligible(const i8conv_shape *shape) {
+  return i8conv_eligible(I8CONV_KERNEL_STRIP, shape);
+}
+
+int i8conv_launch_dispatched(const i8conv_shape *shape, const int8_t *input,
+                             const int8_t *filter, const int32_t *bias,
+                             int32_t *output, void *workspace,
+                             size_t workspace_bytes, void *stream) {
+  const int id = i8conv_dispatch(shape);
+  if (id < 0) {
+    if (shape) derive(*shape, nullptr);  // records the reason
+    return I8CONV_BAD_SHAPE;
+  }
+  return i8conv_launch(id, shape, input, filter, bias, output, workspace,
+                       workspace_bytes, stream);
+}
+
+// ---- runtime layer -------------------------------------------------------
+
+int i8conv_device_count(int *count) {
+  if (!count) return I8CONV_BAD_ARGUMENT;
+  const hipError_t e = hipGetDeviceCount(count);
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipGetDeviceCount", e);
+}
+
+int i8conv_set_device(int device) {
+  const hipError_t e = hipSetDevice(device);
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipSetDevice", e);
+}
+
+int i8conv_device_alloc(void **ptr, size_t bytes) {
+  if (!ptr) return I8CONV_BAD_ARGUMENT;
+  *ptr = nullptr;
+  const hipError_t e = hipMalloc(ptr, bytes ? bytes : 1);
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipMalloc", e);
+}
+
+int i8conv_device_free(void *ptr) {
+  if (!ptr) return I8CONV_OK;
+  const hipError_t e = hipFree(ptr);
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipFree", e);
+}
+
+int i8conv_copy_to_device(void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return I8CONV_OK;
+  const hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipMemcpy H2D", e);
+}
+
+int i8conv_copy_to_host(void *dst, const void *src, size_t bytes) {
+  if (bytes == 0) return I8CONV_OK;
+  const hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipMemcpy D2H", e);
+}
+
+int i8conv_device_fill(void *ptr, int value, size_t bytes) {
+  if (bytes == 0) return I8CONV_OK;
+  hipError_t e = hipMemset(ptr, value, bytes);
+  if (e != hipSuccess) return hip_fail("hipMemset", e);
+  e = hipDeviceSynchronize();
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipDeviceSynchronize", e);
+}
+
+int i8conv_synchronize(void) {
+  const hipError_t e = hipDeviceSynchronize();
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipDeviceSynchronize", e);
+}
+
+int i8conv_stream_create(void **stream) {
+  if (!stream) return I8CONV_BAD_ARGUMENT;
+  hipStream_t s = nullptr;
+  const hipError_t e = hipStreamCreate(&s);  // default priority
+  *stream = s;
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipStreamCreate", e);
+}
+
+int i8conv_stream_destroy(void *stream) {
+  if (!stream) return I8CONV_OK;
+  const hipError_t e = hipStreamDestroy(static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? I8CONV_OK : hip_fail("hipStreamDestroy", e);
+}
+
+int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
+                       size_t name_len) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail("hipGetDevice", e);
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) return hip_fail("hipGetDeviceProperties", e);
+  if (compute_units) *compute_units = prop.multiProcessorCount;
+  if (clock_khz) *clock_khz = prop.clockRate;
+  if (arch_name && name_len) {
+    const std::string n(prop.gcnArchName);
+    const size_t len = std::min(name_len - 1, n.size());
+    n.copy(arch_name, len);
+    arch_name[len] = '\0';
+  }
+  return I8CONV_OK;
+}
+
+int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
+                   const int8_t *filter, const int32_t *bias, int32_t *output,
+                   void *workspace, size_t workspace_bytes, void *stream,
+                   int warmup, int iterations, float *median_ms,
+                   float *batched_ms) {
+  if (warmup < 0 || iterations <= 0 || !median_ms) {
+    set_error("measure needs warmup >= 0, iterations > 0 and an output");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto launch = [&]() {
+    return i8conv_launch(id, shape, input, filter, bias, output, workspace,
+                         workspace_bytes, stream);
+  };
+  for (int i = 0; i < warmup; ++i) {
+    const int rc = launch();
+    if (rc != I8CONV_OK) return rc;
+  }
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail("warmup", e);
+  hipEvent_t start, stop;
+  if ((e = hipEventCreate(&start)) != hipSuccess) return hip_fail("hipEventCreate", e);
+  if ((e = hipEventCreate(&stop)) != hipSuccess) {
+    hipEventDestroy(start);
+    return hip_fail("hipEventCreate", e);
+  }
+  int rc = I8CONV_OK;
+  std::vector<float> samples;
+  samples.reserve(size_t(iterations));
+  for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) {
+    float ms = 0.f;
+    if ((e = hipEventRecord(start, s)) != hipSuccess) { rc = hip_fail("hipEventRecord", e); break; }
+    if ((rc = launch()) != I8CONV_OK) break;
+    if ((e = hipEventRecord(stop, s)) != hipSuccess) { rc = hip_fail("hipEventRecord", e); break; }
+    if ((e = hipEventSynchronize(stop)) != hipSuccess) { rc = hip_fail("hipEventSynchronize", e); break; }
+    if ((e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) { rc = hip_fail("hipEventElapsedTime", e); break; }
+    samples.push_back(ms);
+  }
+  if (rc == I8CONV_OK) {
+    std::sort(samples.begin(), samples.end());
+    *median_ms = samples[samples.size() / 2];
+  }
+  if (rc == I8CONV_OK && batched_ms) {
+    float ms = 0.f;
+    if ((e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+    for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch();
+    if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+    if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
+    if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) rc = hip_fail("hipEventElapsedTime", e);
+    if (rc == I8CONV_OK) *batched_ms = ms / float(iterations);
+  }
+  hipEventDestroy(start);
+  hipEventDestroy(stop);
+  return rc;
+}
+
+const char *i8conv_status_string(int status) {
+  switch (status) {
+    case I8CONV_OK: return "ok";
+    case I8CONV_INELIGIBLE: return "ineligible";
+    case I8CONV_BAD_SHAPE: return "bad shape";
+    case I8CONV_BAD_ARGUMENT: return "bad argument";
+    case I8CONV_WORKSPACE_TOO_SMALL: return "workspace too small";
+    case I8CONV_HIP_ERROR: return "hip error";
+    case I8CONV_UNKNOWN_KERNEL: return "unknown kernel";
+    default: return "unknown status";
+  }
+}
+
+const char *i8conv_last_error(void) { return g_last_error.c_str(); }
+
+}  // extern "C"

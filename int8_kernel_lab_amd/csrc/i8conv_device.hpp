@@ -1,0 +1,120 @@
+// Device-side building blocks shared by every gfx950 kernel of the lab:
+// exact fast division, buffer resources with hardware zero-fill, the INT8
+// MFMA wrapper and the LDS swizzles.  Also compiled by the host (and by g++
+// in the CPU tests) for the parts marked I8_HD.
+#pragma once
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define I8_HD __host__ __device__
+#else
+#define I8_HD
+#endif
+
+namespace i8conv {
+
+// ---------------------------------------------------------------------------
+// Exact unsigned division by a runtime divisor d (1 <= d <= 2^31) for
+// dividends n < 2^31, by multiplication with M = ceil(2^(31+L) / d),
+// L = max(1, ceil(log2 d)).  The round-up method (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994):
+// n*M / 2^(31+L) = n/d + e*n/2^(31+L) with 0 <= e < 1 and
+// e*n/2^(31+L) < 2^-L <= 1/d, so the floor is exactly n/d.
+// 2^31 <= M <= 2^32; M == 2^32 (only d == 1) is stored as add = 1, mul = 0.
+struct FastDiv {
+  uint32_t mul;
+  uint32_t add;
+  uint32_t shift;  // L - 1
+  uint32_t divisor;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{};
+  f.divisor = d;
+  uint32_t l = 1;
+  while (l < 32 && (uint64_t(1) << l) < d) ++l;  // l = max(1, ceil(log2 d))
+  const uint64_t num = uint64_t(1) << (31 + l);
+  const uint64_t m = (num + d - 1) / d;
+  if (m == (uint64_t(1) << 32)) {
+    f.mul = 0;
+    f.add = 1;
+  } else {
+    f.mul = uint32_t(m);
+    f.add = 0;
+  }
+  f.shift = l - 1;
+  return f;
+}
+
+I8_HD inline uint32_t fast_div(uint32_t n, const FastDiv &f) {
+  const uint32_t hi = uint32_t((uint64_t(n) * f.mul) >> 32);
+  return (hi + (f.add ? n : 0u)) >> f.shift;
+}
+
+// Kernel argument block.  All element offsets fit in int32 (the ABI rejects
+// tensors above 2^31-1 bytes).
+struct ConvArgs {
+  const int8_t *x;
+  const int8_t *w;
+  const int32_t *bias;
+  int32_t *y;        // final output (NHWK int32)
+  int32_t *partial;  // split-K partial sums [splits][M][N], else nullptr
+  int n, h, wd, c, k, r, s;
+  int pad_h, pad_w, stride_h, stride_w, dil_h, dil_w;
+  int out_h, out_w;
+  int gemm_m, gemm_n, gemm_k;
+  uint32_t x_bytes, w_bytes;
+  FastDiv div_c, div_s, div_ow, div_ohw;
+  // split-K: stages [split * stages_per_split, ...) of 128 k-bytes each
+  int stages_per_split;
+  int splits;
+};
+
+#if defined(__HIPCC__)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// An offset at or beyond num_records makes a raw buffer load return zeros:
+// that is how padding taps, m >= M and n >= N rows are zero-filled.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base,
+                                                             uint32_t bytes) {
+  // dword3 0x00020000: raw (stride 0) buffer, 32-bit format, gfx9 family.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base),
+                                           (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ v4i load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// D = A x B + C over int8 -> int32.  A is 16 rows (lane % 16) by 64 k,
+// B is 64 k by 16 columns (lane % 16); lane l supplies 16 k-bytes of its
+// row/column for k-block l / 16.  Any mapping of the 64 k positions onto
+// (k-block, byte) is valid as long as A and B use the same one.
+// Result: lane l holds C[4 * (l / 16) + v][l % 16] in element v.
+__device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+#endif  // __HIPCC__
+
+// LDS layout of a [rows][128-byte] operand tile: 16-byte chunk j of row r
+// lives at r*128 + 16*(j ^ (r & 7) ^ ((r >> 3) & 1)).  Sixteen lanes reading
+// chunk j of rows r0..r0+15 (r0 % 16 == 0) hit sixteen distinct 16-byte
+// bank groups modulo 256 bytes, and any eight consecutive ones modulo 128.
+I8_HD inline int swz128(int row, int chunk) {
+  return row * 128 + ((chunk ^ (row & 7) ^ ((row >> 3) & 1)) << 4);
+}
+
+// LDS layout of a [pixels][64-byte] halo/strip patch: chunk j of pixel p at
+// p*64 + 16*(j ^ ((p >> 1) & 3)).  Eight consecutive pixels reading one
+// chunk cover eight distinct 16-byte groups modulo 128 bytes.
+I8_HD inline int swz64(int pixel, int chunk) {
+  return pixel * 64 + ((chunk ^ ((pixel >> 1) & 3)) << 4);
+}
+
+}  // namespace i8conv

@@ -1,0 +1,68 @@
+// Host-side internals shared by the C ABI, the planners and the launchers.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "i8conv.h"
+#include "i8conv_device.hpp"
+
+namespace i8conv {
+
+constexpr int kThreads = 256;      // 4 wave64 per workgroup
+constexpr int kStageBytes = 128;   // k-bytes per LDS stage of the GEMM kernels
+constexpr int kLdsBudget = 160 * 1024;
+
+void set_error(const std::string &message);
+
+// Validity + derived geometry (include/conv_shape.cuh:22-35).
+int derive(const i8conv_shape &s, i8conv_geometry *g);
+
+// ---- generic / split-K -----------------------------------------------------
+// Workgroup tile of the staged implicit GEMM: BM output pixels x BN output
+// channels, k staged 128 bytes at a time.
+struct GemmPlan {
+  int bm = 0, bn = 0;
+  int splits = 1;            // > 1 only for split-K
+  int stages = 0;            // ceil(gemm_k / 128)
+  int stages_per_split = 0;
+};
+bool gemm_tile_supported(int bm, int bn);
+GemmPlan plan_generic(const i8conv_geometry &g);
+GemmPlan plan_splitk(const i8conv_geometry &g);
+size_t splitk_workspace_bytes(const i8conv_geometry &g, const GemmPlan &p);
+
+// ---- halo / strip ----------------------------------------------------------
+// 2-D output tile (th rows x tw columns of one image) x bn output channels.
+// halo : the whole input patch of one 64-channel group is staged in LDS and
+//        reused by all r*s taps.
+// strip: one input row per output row of the tile (filter row fy) is staged
+//        per (channel group, fy) and reused by the s horizontal taps.
+struct PatchPlan {
+  int th = 0, tw = 0, bn = 0;
+  int ph = 0, pw = 0;          // staged region (pixels) of one stage
+  int stage_pixels = 0;        // ph * pw
+  int tiles_y = 0, tiles_x = 0, tiles_n = 0;
+  int frags_m = 0;             // ceil(th * tw / 16)
+  int loads_per_thread = 0;    // 16-byte chunks each thread stages per stage
+  bool strip = false;
+};
+bool plan_halo(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p);
+bool plan_strip(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p);
+
+// Dispatch policy (policy.cpp): an eligible kernel id, or -1 for a bad shape.
+int dispatch(const i8conv_shape &s);
+
+ConvArgs make_args(const i8conv_shape &s, const i8conv_geometry &g,
+                   const int8_t *x, const int8_t *w, const int32_t *bias,
+                   int32_t *y);
+
+// Launchers (asynchronous; return an i8conv_status).
+int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream);
+int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
+                  void *stream);
+int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
+
+}  // namespace i8conv

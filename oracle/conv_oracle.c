@@ -1,0 +1,160 @@
+/*
+ * conv_oracle.c - CPU oracle of the INT8 convolution lab.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the
+ * checker / the timed CPU baseline.  The product (libi8conv.so, conv_lab)
+ * never links or calls it.
+ *
+ * A plain restatement of the reference's CPU INT32 oracle and of the pieces
+ * of its contract that the oracle needs (pthodima/int8_kernel_lab):
+ *   oracle_derive            include/conv_shape.cuh:22-35
+ *   oracle_reference_value   src/conv_lab.cu:39-66
+ *   oracle_conv              reference_value over every output index
+ *   oracle_validate_sampled  src/conv_lab.cu:68-86 (sampling rule)
+ *   oracle_strip_eligible_reference  include/spatial_strip.cuh:11-15
+ * Accumulation is int32 with two's-complement wrap (done in uint32 so that
+ * wrap is defined C), the same as the reference's int32 `sum += x * w` for
+ * every input that does not overflow and the same as the MFMA accumulator.
+ *
+ * Pinning (tests/test_oracle.py): torch.nn.functional.conv2d in float64
+ * fixtures (exact: |acc| < 2^53), brute-force sums on tiny shapes, and
+ * invariants (zero input, one-hot filter, linearity, padding-only taps).
+ */
+#include <pthread.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+typedef struct oracle_shape {
+  int32_t n, h, w, c, k, r, s;
+  int32_t pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w;
+} oracle_shape;
+
+typedef struct oracle_geometry {
+  int32_t out_h, out_w;
+  int64_t gemm_m;
+  int32_t gemm_n, gemm_k;
+  int64_t input_elements, filter_elements, output_elements;
+} oracle_geometry;
+
+/* conv_shape.cuh:22-35: same expressions (C integer division truncates
+ * toward zero, as in the reference's constexpr int arithmetic) and the same
+ * two static_asserts (c % 16 == 0, nonempty output).  Returns 0 on success,
+ * 1 when an assert would fire. */
+int oracle_derive(const oracle_shape *s, oracle_geometry *g) {
+  const int32_t out_h =
+      (s->h + 2 * s->pad_h - s->dilation_h * (s->r - 1) - 1) / s->stride_h + 1;
+  const int32_t out_w =
+      (s->w + 2 * s->pad_w - s->dilation_w * (s->s - 1) - 1) / s->stride_w + 1;
+  if (s->c % 16 != 0) return 1;
+  if (!(out_h > 0 && out_w > 0)) return 1;
+  g->out_h = out_h;
+  g->out_w = out_w;
+  g->gemm_m = (int64_t)s->n * out_h * out_w;
+  g->gemm_n = s->k;
+  g->gemm_k = s->r * s->s * s->c;
+  g->input_elements = (int64_t)s->n * s->h * s->w * s->c;
+  g->filter_elements = (int64_t)s->k * s->r * s->s * s->c;
+  g->output_elements = g->gemm_m * g->gemm_n;
+  return 0;
+}
+
+/* conv_lab.cu:39-66: decode channel = idx % k, then ox, oy, batch; start at
+ * bias[channel]; loop fy -> fx -> c, skipping taps outside the image. */
+int32_t oracle_reference_value(const oracle_shape *S, const int8_t *input,
+                               const int8_t *filter, const int32_t *bias,
+                               int64_t output_index) {
+  oracle_geometry g;
+  oracle_derive(S, &g);
+  const int channel = (int)(output_index % S->k);
+  const int64_t m = output_index / S->k;
+  const int ox = (int)(m % g.out_w);
+  const int oy = (int)((m / g.out_w) % g.out_h);
+  const int batch = (int)(m / ((int64_t)g.out_h * g.out_w));
+  uint32_t sum = (uint32_t)bias[channel];
+  for (int fy = 0; fy < S->r; ++fy) {
+    const int iy = oy * S->stride_h + fy * S->dilation_h - S->pad_h;
+    if (iy < 0 || iy >= S->h) continue;
+    for (int fx = 0; fx < S->s; ++fx) {
+      const int ix = ox * S->stride_w + fx * S->dilation_w - S->pad_w;
+      if (ix < 0 || ix >= S->w) continue;
+      const int8_t *xp = input + (((int64_t)batch * S->h + iy) * S->w + ix) * S->c;
+      const int8_t *wp = filter + (((int64_t)channel * S->r + fy) * S->s + fx) * S->c;
+      int32_t dot = 0; /* |dot| <= c * 2^14 < 2^31 for c < 2^17 */
+      for (int c = 0; c < S->c; ++c) dot += (int32_t)xp[c] * (int32_t)wp[c];
+      sum += (uint32_t)dot;
+    }
+  }
+  return (int32_t)sum;
+}
+
+typedef struct {
+  const oracle_shape *s;
+  const int8_t *x;
+  const int8_t *w;
+  const int32_t *b;
+  int32_t *out;
+  int64_t begin, end;
+} oracle_job;
+
+static void *oracle_worker(void *arg) {
+  const oracle_job *j = (const oracle_job *)arg;
+  for (int64_t i = j->begin; i < j->end; ++i)
+    j->out[i] = oracle_reference_value(j->s, j->x, j->w, j->b, i);
+  return NULL;
+}
+
+/* Every output element, split statically over `threads` POSIX threads (in
+ * contiguous ranges of output indices).  Returns 0, or 1 for a bad shape. */
+int oracle_conv(const oracle_shape *s, const int8_t *input, const int8_t *filter,
+                const int32_t *bias, int32_t *output, int threads) {
+  oracle_geometry g;
+  if (oracle_derive(s, &g)) return 1;
+  const int64_t total = g.output_elements;
+  if (threads < 1) threads = 1;
+  if (threads > 256) threads = 256;
+  pthread_t tid[256];
+  int spawned[256];
+  oracle_job jobs[256];
+  for (int t = 0; t < threads; ++t) {
+    jobs[t].s = s;
+    jobs[t].x = input;
+    jobs[t].w = filter;
+    jobs[t].b = bias;
+    jobs[t].out = output;
+    jobs[t].begin = total * t / threads;
+    jobs[t].end = total * (t + 1) / threads;
+    spawned[t] = t < threads - 1 &&
+                 pthread_create(&tid[t], NULL, oracle_worker, &jobs[t]) == 0;
+    if (!spawned[t]) oracle_worker(&jobs[t]); /* last range, or a failed spawn */
+  }
+  for (int t = 0; t < threads; ++t)
+    if (spawned[t]) pthread_join(tid[t], NULL);
+  return 0;
+}
+
+/* conv_lab.cu:68-86: full comparison when output_elements <= 65536, else
+ * 2048 samples at index sample * output_elements / 2048.  Returns the first
+ * mismatching index, or -1 when every sampled output matches. */
+int64_t oracle_validate_sampled(const oracle_shape *s, const int8_t *input,
+                                const int8_t *filter, const int32_t *bias,
+                                const int32_t *output) {
+  oracle_geometry g;
+  if (oracle_derive(s, &g)) return 0;
+  const int64_t total = g.output_elements;
+  const int64_t samples = total <= 65536 ? total : 2048;
+  for (int64_t k = 0; k < samples; ++k) {
+    const int64_t idx = samples == total ? k : k * total / samples;
+    if (output[idx] != oracle_reference_value(s, input, filter, bias, idx)) return idx;
+  }
+  return -1;
+}
+
+/* spatial_strip.cuh:11-15, the reference's own strip predicate. */
+int oracle_strip_eligible_reference(const oracle_shape *s) {
+  oracle_geometry g;
+  if (oracle_derive(s, &g)) return 0;
+  return s->r == 3 && s->s == 3 && s->stride_w == 1 && s->dilation_w == 1 &&
+         s->c % 64 == 0 && s->k % 64 == 0 && g.out_w % 128 == 0;
+}

@@ -1,0 +1,101 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+Each function cites the reference code it restates (see conv_oracle.c).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_int, c_int32, c_int64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+FIELDS = ("n", "h", "w", "c", "k", "r", "s", "pad_h", "pad_w",
+          "stride_h", "stride_w", "dilation_h", "dilation_w")
+
+
+class OShape(ctypes.Structure):
+    _fields_ = [(f, c_int32) for f in FIELDS]
+
+
+class OGeometry(ctypes.Structure):
+    _fields_ = [("out_h", c_int32), ("out_w", c_int32), ("gemm_m", c_int64),
+                ("gemm_n", c_int32), ("gemm_k", c_int32), ("input_elements", c_int64),
+                ("filter_elements", c_int64), ("output_elements", c_int64)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        h = ctypes.CDLL(LIB_PATH)
+        h.oracle_derive.restype = c_int
+        h.oracle_derive.argtypes = [POINTER(OShape), POINTER(OGeometry)]
+        h.oracle_reference_value.restype = c_int32
+        h.oracle_reference_value.argtypes = [POINTER(OShape), c_void_p, c_void_p, c_void_p, c_int64]
+        h.oracle_conv.restype = c_int
+        h.oracle_conv.argtypes = [POINTER(OShape), c_void_p, c_void_p, c_void_p, c_void_p, c_int]
+        h.oracle_validate_sampled.restype = c_int64
+        h.oracle_validate_sampled.argtypes = [POINTER(OShape), c_void_p, c_void_p, c_void_p, c_void_p]
+        h.oracle_strip_eligible_reference.restype = c_int
+        h.oracle_strip_eligible_reference.argtypes = [POINTER(OShape)]
+        _lib = h
+    return _lib
+
+
+def _shape(shape) -> OShape:
+    return OShape(*[int(getattr(shape, f)) for f in FIELDS])
+
+
+def derive(shape):
+    """conv_shape.cuh:22-35 -> OGeometry, or None where a static_assert fires."""
+    g = OGeometry()
+    return None if lib().oracle_derive(ctypes.byref(_shape(shape)), ctypes.byref(g)) else g
+
+
+def _arrays(x, w, b):
+    return (np.ascontiguousarray(x, dtype=np.int8), np.ascontiguousarray(w, dtype=np.int8),
+            np.ascontiguousarray(b, dtype=np.int32))
+
+
+def reference_value(shape, x, w, b, index: int) -> int:
+    """conv_lab.cu:39-66 for one output index."""
+    x, w, b = _arrays(x, w, b)
+    return int(lib().oracle_reference_value(ctypes.byref(_shape(shape)), x.ctypes.data,
+                                            w.ctypes.data, b.ctypes.data, int(index)))
+
+
+def conv(shape, x, w, b, threads: int = 0) -> np.ndarray:
+    """reference_value for every output index -> NHWK int32 array."""
+    g = derive(shape)
+    if g is None:
+        raise ValueError(f"bad shape {shape}")
+    x, w, b = _arrays(x, w, b)
+    out = np.empty(g.output_elements, dtype=np.int32)
+    threads = threads or min(16, os.cpu_count() or 1)
+    rc = lib().oracle_conv(ctypes.byref(_shape(shape)), x.ctypes.data, w.ctypes.data,
+                           b.ctypes.data, out.ctypes.data, int(threads))
+    assert rc == 0
+    return out.reshape(shape.n, g.out_h, g.out_w, shape.k)
+
+
+def validate_sampled(shape, x, w, b, output) -> int:
+    """conv_lab.cu:68-86 sampling rule; first mismatching index or -1."""
+    x, w, b = _arrays(x, w, b)
+    out = np.ascontiguousarray(output, dtype=np.int32)
+    return int(lib().oracle_validate_sampled(ctypes.byref(_shape(shape)), x.ctypes.data,
+                                             w.ctypes.data, b.ctypes.data, out.ctypes.data))
+
+
+def strip_eligible_reference(shape) -> bool:
+    """spatial_strip.cuh:11-15 (the reference's predicate, not the gfx950 one)."""
+    return bool(lib().oracle_strip_eligible_reference(ctypes.byref(_shape(shape))))

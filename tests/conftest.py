@@ -1,0 +1,47 @@
+"""Shared test setup.
+
+* registers the ``gpu`` marker (tests that need an MI355X);
+* puts the repository root on sys.path;
+* builds libi8conv.so / liboracle.so only when they are missing (the GPU box
+  runs the prebuilt files and never builds).
+"""
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+LIB = os.path.join(ROOT, "int8_kernel_lab_amd", "libi8conv.so")
+DRIVER = os.path.join(ROOT, "int8_kernel_lab_amd", "conv_lab")
+ORACLE = os.path.join(ROOT, "oracle", "liboracle.so")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+def _build_if_missing():
+    if not os.path.exists(ORACLE):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True)
+    if not (os.path.exists(LIB) and os.path.exists(DRIVER)):
+        subprocess.run(["make", "-j8", "-C", os.path.join(ROOT, "int8_kernel_lab_amd", "csrc")],
+                       check=True)
+
+
+_build_if_missing()
+
+
+def say(msg: str) -> None:
+    """Names the case before each GPU step (flushed, so a fault still shows it)."""
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="session")
+def baseline_cases():
+    import int8_kernel_lab_amd as lab
+    return lab.load_workloads(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"))

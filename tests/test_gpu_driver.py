@@ -1,0 +1,58 @@
+"""GPU runs of the C++ host driver (conv_lab): oracle check before timing,
+CSV row with the reference's columns first, exit code contract."""
+import csv
+import io
+import os
+import subprocess
+
+import pytest
+
+from tests.conftest import DRIVER, say
+
+REF_COLUMNS = ["case", "n", "h", "w", "c", "k", "r", "s", "out_h", "out_w", "eligible_strip",
+               "generic_ms", "strip_ms", "winner", "generic_correct", "strip_correct"]
+
+
+def run_driver(*args, timeout=120):
+    return subprocess.run([DRIVER, *args], capture_output=True, text=True, timeout=timeout)
+
+
+@pytest.mark.gpu
+def test_driver_all_kernels_csv_on_smoke():
+    say("[gpu] conv_lab --strategy all --csv --case cfg1_smoke")
+    p = run_driver("--strategy", "all", "--csv", "--case", "cfg1_smoke", "--warmup", "2",
+                   "--iterations", "5")
+    assert p.returncode == 0, p.stderr
+    rows = list(csv.DictReader(io.StringIO(p.stdout)))
+    assert len(rows) == 1
+    row = rows[0]
+    header = p.stdout.splitlines()[0].split(",")
+    assert header[:len(REF_COLUMNS)] == REF_COLUMNS  # conv_lab.cu:223-224 prefix
+    for k in ("generic", "strip", "halo", "splitk"):
+        assert row[f"{k}_correct"] == "1"
+        assert float(row[f"{k}_ms"]) > 0
+    assert row["winner"] in ("generic", "strip", "halo", "splitk")
+    assert row["out_h"] == "16" and row["out_w"] == "16"
+
+
+@pytest.mark.gpu
+def test_driver_reference_strategy_both_on_stride2():
+    # strip is ineligible at stride 2: its column stays -1, as in the
+    # reference (conv_lab.cu:180-181, 197), and the winner is generic
+    say("[gpu] conv_lab --strategy both --csv --case cfg3_down_3x3_s2")
+    p = run_driver("--strategy", "both", "--csv", "--case", "cfg3_down_3x3_s2", "--warmup", "2",
+                   "--iterations", "5")
+    assert p.returncode == 0, p.stderr
+    row = next(csv.DictReader(io.StringIO(p.stdout)))
+    assert row["eligible_strip"] == "0"
+    assert float(row["strip_ms"]) == -1
+    assert row["winner"] == "generic"
+
+
+@pytest.mark.gpu
+def test_driver_human_line_and_reference_value_range():
+    say("[gpu] conv_lab --range reference --case cfg4b_k36_tail")
+    p = run_driver("--range", "reference", "--case", "cfg4b_k36_tail", "--strategy", "dispatch",
+                   "--warmup", "1", "--iterations", "3")
+    assert p.returncode == 0, p.stderr
+    assert p.stdout.startswith("cfg4b_k36_tail:") and "winner" in p.stdout

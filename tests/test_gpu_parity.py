@@ -1,0 +1,168 @@
+"""GPU parity: every candidate kernel, bit-exact against the CPU oracle.
+
+Each check poisons the output buffer first (so a kernel that skips stores
+cannot pass on stale data), launches through the C ABI, and compares EVERY
+output element with oracle.conv (the restatement of conv_lab.cu:39-66).
+The reference checked 2048 sampled outputs (conv_lab.cu:72-77).
+"""
+import numpy as np
+import pytest
+
+import int8_kernel_lab_amd as lab
+from oracle import oracle
+from tests.conftest import say
+
+BASELINE_NAMES = ["cfg1_smoke", "cfg2_resnet_3x3_s1", "cfg3_down_3x3_s2",
+                  "cfg4a_pointwise_1x1", "cfg4b_k36_tail", "cfg5a_deep_k", "cfg5b_dilated"]
+
+# Edge shapes the reference's tests never reached (its sampled check and
+# compile-time predicate hid them): odd and non-multiple-of-4 K, C = 16/48,
+# asymmetric filters, stride 2/4, 5x5, dilation with taps outside the image,
+# a 1x1 image, the truncating out_h formula, rows wider than one tile,
+# multi-tile K with a tail, M tails.
+EDGE = {
+    "k63": lab.ConvShape(1, 18, 18, 64, 63, 3, 3, 1, 1, 1, 1, 1, 1),
+    "k69_s2": lab.ConvShape(2, 17, 19, 64, 69, 3, 3, 1, 1, 2, 2, 1, 1),
+    "c16_1x1_k5": lab.ConvShape(3, 9, 7, 16, 5, 1, 1, 0, 0, 1, 1, 1, 1),
+    "c48_3x3": lab.ConvShape(2, 10, 12, 48, 24, 3, 3, 1, 1, 1, 1, 1, 1),
+    "asym_1x3": lab.ConvShape(2, 16, 16, 64, 32, 1, 3, 0, 1, 1, 1, 1, 1),
+    "asym_3x1": lab.ConvShape(2, 16, 16, 64, 32, 3, 1, 1, 0, 1, 1, 1, 1),
+    "k5x5_s2": lab.ConvShape(2, 23, 23, 64, 40, 5, 5, 2, 2, 2, 2, 1, 1),
+    "patch4x4_s4": lab.ConvShape(2, 32, 32, 32, 96, 4, 4, 0, 0, 4, 4, 1, 1),
+    "dil3_pad1": lab.ConvShape(1, 20, 20, 64, 64, 3, 3, 1, 1, 1, 1, 3, 3),
+    "one_pixel": lab.ConvShape(2, 1, 1, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    "trunc_out": lab.ConvShape(1, 2, 2, 16, 8, 3, 3, 0, 0, 2, 2, 1, 1),
+    "wide_row": lab.ConvShape(1, 3, 200, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    "deep_c": lab.ConvShape(1, 5, 5, 1024, 80, 3, 3, 1, 1, 1, 1, 1, 1),
+    "k300": lab.ConvShape(1, 8, 8, 64, 300, 3, 3, 1, 1, 1, 1, 1, 1),
+    "m_tail": lab.ConvShape(3, 7, 9, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
+    "s2_dil2": lab.ConvShape(2, 30, 30, 64, 64, 3, 3, 2, 2, 2, 2, 2, 2),
+}
+
+_expected_cache = {}
+
+
+def _case(name, shape, seed=lab.BASELINE_SEED):
+    key = (name, shape, seed)
+    if key not in _expected_cache:
+        x, w, b = lab.make_case_data(shape, seed)
+        _expected_cache.clear()  # keep one case resident (config 5b is 34 MB)
+        _expected_cache[key] = (x, w, b, oracle.conv(shape, x, w, b))
+    return _expected_cache[key]
+
+
+def run_kernel(kernel, shape, x, w, b, poison=0xA5):
+    """Poisoned output -> launch -> synchronize -> host copy."""
+    g = shape.geometry()
+    xb = lab.DeviceBuffer.from_array(x)
+    wb = lab.DeviceBuffer.from_array(w)
+    bb = lab.DeviceBuffer.from_array(b)
+    yb = lab.DeviceBuffer(4 * g.output_elements)
+    ws_n = lab.workspace_bytes(kernel, shape)
+    ws = lab.DeviceBuffer(ws_n) if ws_n else None
+    try:
+        yb.fill(poison)
+        if ws is not None:
+            ws.fill(0x5A)
+        lab.launch(kernel, shape, xb, wb, bb, yb, ws, ws_n)
+        lab.synchronize()
+        return yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
+    finally:
+        for buf in (xb, wb, bb, yb, ws):
+            if buf is not None:
+                buf.close()
+
+
+def assert_bit_exact(got, expected, label):
+    if not np.array_equal(got, expected):
+        bad = np.argwhere(got != expected)
+        first = tuple(int(v) for v in bad[0])
+        raise AssertionError(f"{label}: {len(bad)} mismatches; first at NHWK {first}: "
+                             f"expected {int(expected[first])}, got {int(got[first])}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kernel", lab.KERNELS)
+@pytest.mark.parametrize("case", BASELINE_NAMES)
+def test_baseline_config_bit_exact(case, kernel, baseline_cases):
+    shape = baseline_cases[case]
+    if not lab.eligible(kernel, shape):
+        pytest.skip(f"{kernel} ineligible for {case}")
+    x, w, b, expected = _case(case, shape)
+    say(f"[gpu] {kernel} on {case} {shape}")
+    got = run_kernel(kernel, shape, x, w, b)
+    assert_bit_exact(got, expected, f"{kernel}/{case}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kernel", lab.KERNELS)
+@pytest.mark.parametrize("case", sorted(EDGE))
+def test_edge_shape_bit_exact(case, kernel):
+    shape = EDGE[case]
+    if not lab.eligible(kernel, shape):
+        pytest.skip(f"{kernel} ineligible for {case}")
+    x, w, b, expected = _case(case, shape, seed=7)
+    say(f"[gpu] {kernel} on edge {case} {shape}")
+    got = run_kernel(kernel, shape, x, w, b)
+    assert_bit_exact(got, expected, f"{kernel}/{case}")
+
+
+@pytest.mark.gpu
+def test_dispatched_kernel_matches_on_every_baseline_config(baseline_cases):
+    for case in BASELINE_NAMES:
+        shape = baseline_cases[case]
+        kernel = lab.dispatch(shape)
+        x, w, b, expected = _case(case, shape)
+        say(f"[gpu] dispatch -> {kernel} on {case}")
+        got = lab.conv2d(x, w, b, shape)
+        assert_bit_exact(got, expected, f"dispatch({kernel})/{case}")
+
+
+@pytest.mark.gpu
+def test_extreme_values_do_not_lose_bits():
+    # all -128 input and filter: every product is +16384, the largest
+    # magnitude an int8 x int8 product reaches; C = 2048, 3x3 -> |acc| near
+    # 3.0e8 plus bias 2^20 (configuration 5a's worst case).
+    shape = lab.ConvShape(1, 7, 7, 2048, 64, 3, 3, 1, 1, 1, 1, 1, 1)
+    x = np.full((1, 7, 7, 2048), -128, np.int8)
+    w = np.full((64, 3, 3, 2048), -128, np.int8)
+    b = np.full(64, (1 << 20), np.int32)
+    expected = oracle.conv(shape, x, w, b)
+    assert int(expected.max()) == 9 * 2048 * 16384 + (1 << 20)
+    for kernel in lab.KERNELS:
+        if not lab.eligible(kernel, shape):
+            continue
+        say(f"[gpu] {kernel} on extreme values")
+        assert_bit_exact(run_kernel(kernel, shape, x, w, b), expected, f"{kernel}/extreme")
+
+
+@pytest.mark.gpu
+def test_split_k_is_deterministic(baseline_cases):
+    shape = baseline_cases["cfg5a_deep_k"]
+    x, w, b, expected = _case("cfg5a_deep_k", shape)
+    say("[gpu] splitk twice on cfg5a_deep_k (different poison)")
+    first = run_kernel("splitk", shape, x, w, b, poison=0x00)
+    second = run_kernel("splitk", shape, x, w, b, poison=0xFF)
+    assert first.tobytes() == second.tobytes()
+    assert_bit_exact(first, expected, "splitk/cfg5a")
+
+
+@pytest.mark.gpu
+def test_launch_errors_are_statuses_not_faults(baseline_cases):
+    shape = baseline_cases["cfg3_down_3x3_s2"]  # stride 2: strip ineligible
+    g = shape.geometry()
+    xb = lab.DeviceBuffer(g.input_elements)
+    wb = lab.DeviceBuffer(g.filter_elements)
+    bb = lab.DeviceBuffer(4 * shape.k)
+    yb = lab.DeviceBuffer(4 * g.output_elements)
+    try:
+        with pytest.raises(lab.I8ConvError, match="ineligible"):
+            lab.launch("strip", shape, xb, wb, bb, yb)
+        with pytest.raises(lab.I8ConvError, match="workspace too small"):
+            lab.launch("splitk", shape, xb, wb, bb, yb, None, 0)
+        with pytest.raises(lab.I8ConvError, match="bad argument"):
+            lab.launch("generic", shape, xb.ptr + 1, wb, bb, yb)  # misaligned input
+        lab.synchronize()
+    finally:
+        for buf in (xb, wb, bb, yb):
+            buf.close()
