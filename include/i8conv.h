@@ -98,6 +98,11 @@ int i8conv_eligible(int id, const i8conv_shape *shape);
 /* Device workspace a launch of `id` on `shape` needs, in bytes (0 for all
  * kernels but split-K).  0 also for an ineligible shape. */
 size_t i8conv_workspace_bytes(int id, const i8conv_shape *shape);
+/* Writes a one-line description of the tile plan kernel `id` would use for
+ * `shape` (variant, tile, grid) into buf (NUL-terminated, at most len
+ * bytes).  I8CONV_INELIGIBLE / I8CONV_BAD_SHAPE when there is none.  No
+ * reference counterpart: it reports the launch geometry for logs and CSVs. */
+int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len);
 
 /* ---- dispatch policy (kept outside the kernels) ------------------------ */
 

@@ -30,7 +30,7 @@ from . import _lib
 from ._lib import I8ConvError, check, lib
 
 __all__ = [
-    "ConvShape", "DeviceBuffer", "I8ConvError", "KERNELS", "conv2d", "dispatch",
+    "ConvShape", "DeviceBuffer", "I8ConvError", "KERNELS", "conv2d", "describe", "dispatch",
     "eligible", "fill_int8", "fill_int32", "kernel_names", "launch",
     "launch_generic", "launch_spatial_strip", "load_case", "load_workloads",
     "make_case_data", "measure", "spatial_strip_eligible", "workspace_bytes",
@@ -170,6 +170,14 @@ def spatial_strip_eligible(shape: ConvShape) -> bool:
 
 def workspace_bytes(name: str, shape: ConvShape) -> int:
     return int(lib().i8conv_workspace_bytes(_kernel_id(name), ctypes.byref(shape.c_struct())))
+
+
+def describe(name: str, shape: ConvShape) -> str:
+    """One-line description of the tile plan `name` would launch for `shape`."""
+    buf = ctypes.create_string_buffer(256)
+    check(lib().i8conv_describe(_kernel_id(name), ctypes.byref(shape.c_struct()), buf, 256),
+          f"describe {name}")
+    return buf.value.decode()
 
 
 def dispatch(shape: ConvShape) -> str:

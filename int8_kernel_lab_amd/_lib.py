@@ -48,6 +48,7 @@ SIGNATURES = {
     "i8conv_kernel_id": (c_int, [c_char_p]),
     "i8conv_eligible": (c_int, [c_int, POINTER(CShape)]),
     "i8conv_workspace_bytes": (c_size_t, [c_int, POINTER(CShape)]),
+    "i8conv_describe": (c_int, [c_int, POINTER(CShape), c_char_p, c_size_t]),
     "i8conv_dispatch": (c_int, [POINTER(CShape)]),
     "i8conv_dispatch_workspace_bytes": (c_size_t, [POINTER(CShape)]),
     "i8conv_launch": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,

@@ -75,6 +75,45 @@ size_t i8conv_workspace_bytes(int id, const i8conv_shape *shape) {
   return splitk_workspace_bytes(g, plan_splitk(g));
 }
 
+int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
+  if (!shape || !buf || len == 0) return I8CONV_BAD_ARGUMENT;
+  buf[0] = '\0';
+  if (id < 0 || id >= I8CONV_KERNEL_COUNT) return I8CONV_UNKNOWN_KERNEL;
+  i8conv_geometry g;
+  const int rc = derive(*shape, &g);
+  if (rc != I8CONV_OK) return rc;
+  if (!i8conv_eligible(id, shape)) return I8CONV_INELIGIBLE;
+  std::string d;
+  auto tiles = [](int64_t a, int64_t b) { return std::to_string((a + b - 1) / b); };
+  if (id == I8CONV_KERNEL_GENERIC || id == I8CONV_KERNEL_SPLITK) {
+    const GemmPlan p = id == I8CONV_KERNEL_GENERIC ? plan_generic(g) : plan_splitk(g);
+    d = std::string(kNames[id]) + " tile " + std::to_string(p.bm) + "px x " +
+        std::to_string(p.bn) + "oc, grid " + tiles(g.gemm_m, p.bm) + "x" +
+        tiles(g.gemm_n, p.bn) + (p.splits > 1 ? "x" + std::to_string(p.splits) + " splits" : "") +
+        ", " + std::to_string(p.stages) + " k-stages";
+  } else {
+    PatchPlan p;
+    if (id == I8CONV_KERNEL_STRIP) plan_strip(*shape, g, &p);
+    else plan_halo(*shape, g, &p);
+    if (p.resident) {
+      d = std::string(kNames[id]) + " resident rows: " + std::to_string(p.ranges) +
+          " pixel ranges of <=" + std::to_string(p.frags_m * 16) + "px x " +
+          std::to_string(p.bn) + "oc, LDS " +
+          std::to_string(size_t(shape->c / 64) * p.copies * 4) + " KB, grid " +
+          std::to_string(int64_t(p.ranges) * p.tiles_n);
+    } else {
+      d = std::string(kNames[id]) + " tile " + std::to_string(p.th) + "x" +
+          std::to_string(p.tw) + "px x " + std::to_string(p.bn) + "oc, staged " +
+          std::to_string(p.ph) + "x" + std::to_string(p.pw) + "px, grid " +
+          std::to_string(int64_t(shape->n) * p.tiles_y * p.tiles_x * p.tiles_n);
+    }
+  }
+  const size_t n = std::min(len - 1, d.size());
+  d.copy(buf, n);
+  buf[n] = '\0';
+  return I8CONV_OK;
+}
+
 int i8conv_dispatch(const i8conv_shape *shape) {
   if (!shape) return -1;
   return dispatch(*shape);
@@ -121,7 +160,8 @@ int i8conv_launch(int id, const i8conv_shape *shape, const int8_t *input,
         set_error(std::string(kNames[id]) + " is not eligible for this shape");
         return I8CONV_INELIGIBLE;
       }
-      return launch_patch(args, pp, stream);
+      return pp.resident ? launch_halo_resident(args, pp, stream)
+                         : launch_patch(args, pp, stream);
     }
     case I8CONV_KERNEL_SPLITK: {
       if (!i8conv_eligible(id, shape)) {

@@ -342,6 +342,10 @@ int main(int argc, char **argv) {
   const double gbps = best_ms > 0 ? bytes / (best_ms * 1e-3) / 1e9 : -1.0;
   const double hbm_gbps = 8000.0;   // MI355X HBM3E, published
 
+  char plan_buf[256] = {0};
+  if (dispatched >= 0) i8conv_describe(dispatched, &shape, plan_buf, sizeof(plan_buf));
+  std::string plan(plan_buf);
+  std::replace(plan.begin(), plan.end(), ',', ';');  // keep the CSV row flat
   const Result &gr = res[I8CONV_KERNEL_GENERIC];
   const Result &sr = res[I8CONV_KERNEL_STRIP];
   const Result &hr = res[I8CONV_KERNEL_HALO];
@@ -354,7 +358,7 @@ int main(int argc, char **argv) {
                    "pad_h,pad_w,stride_h,stride_w,dilation_h,dilation_w,"
                    "eligible_halo,halo_ms,halo_correct,eligible_splitk,splitk_ms,"
                    "splitk_correct,dispatch,winner_batched_ms,tops,pct_int8_peak,gbps,"
-                   "pct_hbm,cpu_check_ms,cpu_threads,device,cus\n";
+                   "pct_hbm,cpu_check_ms,cpu_threads,device,cus,dispatch_plan\n";
     std::cout << opt.name << ',' << shape.n << ',' << shape.h << ',' << shape.w << ','
               << shape.c << ',' << shape.k << ',' << shape.r << ',' << shape.s << ','
               << g.out_h << ',' << g.out_w << ',' << (sr.eligible ? 1 : 0) << ','
@@ -369,7 +373,7 @@ int main(int argc, char **argv) {
               << fmt(winner >= 0 ? res[size_t(winner)].batched_ms : -1.f) << ','
               << std::setprecision(6) << tops << ',' << (tops > 0 ? 100.0 * tops / peak_tops : -1.0)
               << ',' << gbps << ',' << (gbps > 0 ? 100.0 * gbps / hbm_gbps : -1.0) << ','
-              << cpu_ms << ',' << threads << ',' << arch << ',' << cus << '\n';
+              << cpu_ms << ',' << threads << ',' << arch << ',' << cus << ',' << plan << '\n';
   } else {
     std::cout << opt.name << ":";
     for (int id : run) {

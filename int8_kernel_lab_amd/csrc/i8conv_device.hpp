@@ -111,10 +111,15 @@ I8_HD inline int swz128(int row, int chunk) {
 }
 
 // LDS layout of a [pixels][64-byte] halo/strip patch: chunk j of pixel p at
-// p*64 + 16*(j ^ ((p >> 1) & 3)).  Eight consecutive pixels reading one
-// chunk cover eight distinct 16-byte groups modulo 128 bytes.
+// p*64 + 16*(j ^ ((p >> 2) & 3)).  Sixteen consecutive pixels reading one
+// chunk (the 16 lanes of an MFMA fragment) cover all sixteen 16-byte bank
+// groups of gfx950's 64 x 4-byte LDS banks.
 I8_HD inline int swz64(int pixel, int chunk) {
-  return pixel * 64 + ((chunk ^ ((pixel >> 1) & 3)) << 4);
+  return pixel * 64 + ((chunk ^ ((pixel >> 2) & 3)) << 4);
 }
+// Inverse: the logical chunk stored in physical 16-byte slot `phys` of
+// `pixel` (used when a DMA writes slots in order and each lane must fetch
+// the chunk its slot holds).
+I8_HD inline int swz64_chunk(int pixel, int phys) { return phys ^ ((pixel >> 2) & 3); }
 
 }  // namespace i8conv

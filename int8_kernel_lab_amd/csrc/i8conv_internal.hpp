@@ -48,6 +48,11 @@ struct PatchPlan {
   int frags_m = 0;             // ceil(th * tw / 16)
   int loads_per_thread = 0;    // 16-byte chunks each thread stages per stage
   bool strip = false;
+  // halo only: flattened pixel ranges with their input rows of every channel
+  // group resident in LDS and the filter slice in registers (kernel_halo.hip)
+  bool resident = false;
+  int ranges = 0;  // resident: pixel ranges per channel slice
+  int copies = 0;  // resident: 1 KB LDS copies per wave per channel group
 };
 bool plan_halo(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p);
 bool plan_strip(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p);
@@ -64,5 +69,9 @@ int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream);
 int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
                   void *stream);
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
+int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
+// Whether kernel_halo.hip has an instance for 16*fn channels per wave and
+// `steps` 64-byte k-steps.
+bool halo_instance_exists(int fn, int steps);
 
 }  // namespace i8conv

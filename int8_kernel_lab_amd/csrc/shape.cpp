@@ -122,8 +122,63 @@ namespace {
 constexpr int kMaxTilePixels = 128;   // 8 MFMA column fragments
 constexpr int kMaxStagePixels = 768;  // 12 staged 16-byte chunks per thread
 
+enum class PatchMode { kStagedHalo, kStrip };
+
+// Resident-halo plan (kernel_halo.hip).  The filter slice of a wave
+// (16*fn channels x gemm_k bytes) must match an instantiated kernel, and
+// every tap of every output pixel must land inside the zero-padded image
+// (true unless out_h/out_w come from the truncating formula with a negative
+// numerator).  Ranges: as few as fill the compute units once, more while
+// the input rows of the longest range do not fit LDS.
+bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
+  if (s.c % 64 != 0 || g.gemm_k % 64 != 0) return false;
+  const int steps = g.gemm_k / 64;
+  const int fn = (s.k > 64 && halo_instance_exists(2, steps)) ? 2 : 1;
+  if (!halo_instance_exists(fn, steps)) return false;
+  const int hp = s.h + 2 * s.pad_h;
+  const int wp = s.w + 2 * s.pad_w;
+  if (int64_t(g.out_h - 1) * s.stride_h + int64_t(s.r - 1) * s.dilation_h >= hp) return false;
+  if (int64_t(g.out_w - 1) * s.stride_w + int64_t(s.s - 1) * s.dilation_w >= wp) return false;
+  const int64_t total_frags = ceil_div(g.gemm_m, 16);
+  const int tiles_n = int(ceil_div(s.k, 64 * fn));
+  auto vrow = [&](int64_t m) {
+    const int64_t b = m / (int64_t(g.out_h) * g.out_w);
+    const int64_t oy = (m % (int64_t(g.out_h) * g.out_w)) / g.out_w;
+    return b * hp + oy * s.stride_h;
+  };
+  for (int64_t ranges = std::max<int64_t>(1, std::min(total_frags, ceil_div(256, tiles_n)));
+       ranges <= total_frags; ranges = std::min(total_frags, ranges * 5 / 4 + 1)) {
+    int64_t max_slots = 0;
+    for (int64_t r = 0; r < ranges; ++r) {
+      const int64_t f0 = r * total_frags / ranges, f1 = (r + 1) * total_frags / ranges;
+      if (f1 <= f0) continue;
+      const int64_t m0 = f0 * 16, m1 = std::min<int64_t>(f1 * 16, g.gemm_m) - 1;
+      const int64_t rows = vrow(m1) - vrow(m0) + int64_t(s.r - 1) * s.dilation_h + 1;
+      max_slots = std::max(max_slots, rows * wp);
+    }
+    const int64_t copies = ceil_div(max_slots * 4, kThreads);  // 4 waves x 64 slots
+    const int64_t lds = int64_t(s.c / 64) * copies * 4096;
+    if (lds <= kLdsBudget && ranges * tiles_n <= INT32_MAX) {
+      p->resident = true;
+      p->strip = false;
+      p->bn = 64 * fn;
+      p->tiles_n = tiles_n;
+      p->ranges = int(ranges);
+      p->copies = int(copies);
+      p->frags_m = int(ceil_div(total_frags, ranges));
+      p->th = p->tw = p->ph = p->pw = 0;
+      p->tiles_y = p->tiles_x = 1;
+      p->stage_pixels = int(max_slots);
+      return true;
+    }
+    if (ranges == total_frags) break;
+  }
+  return false;
+}
+
 bool finish_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
-                       PatchPlan *p) {
+                       PatchMode mode, PatchPlan *p) {
+  (void)mode;
   p->stage_pixels = p->ph * p->pw;
   if (p->stage_pixels > kMaxStagePixels) return false;
   if (size_t(2) * p->stage_pixels * 64 > size_t(kLdsBudget)) return false;
@@ -140,7 +195,7 @@ bool finish_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
 // when out_w <= 128) whose staged region fits, preferring pixel counts that
 // fill whole 16-column MFMA fragments.
 bool search_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
-                       bool strip, PatchPlan *out) {
+                       PatchMode mode, int bn, PatchPlan *out) {
   PatchPlan best;
   bool found = false;
   double best_score = -1.0;
@@ -150,18 +205,18 @@ bool search_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
     const int th_max = std::min(g.out_h, kMaxTilePixels / tw);
     for (int th = th_max; th >= 1; --th) {
       PatchPlan p;
-      p.strip = strip;
+      p.strip = mode == PatchMode::kStrip;
       p.th = th;
       p.tw = tw;
-      p.bn = s.k > 64 ? 128 : 64;
-      if (strip) {
+      p.bn = bn;
+      if (p.strip) {
         p.ph = th;
         p.pw = tw + s.s - 1;
       } else {
         p.ph = (th - 1) * s.stride_h + (s.r - 1) * s.dilation_h + 1;
         p.pw = (tw - 1) * s.stride_w + (s.s - 1) * s.dilation_w + 1;
       }
-      if (!finish_patch_plan(s, g, &p)) continue;
+      if (!finish_patch_plan(s, g, mode, &p)) continue;
       const int px = th * tw;
       // useful fraction of the MFMA columns the whole grid computes (edge
       // tiles included), times a mild preference for big tiles (less halo
@@ -184,10 +239,15 @@ bool search_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
 }  // namespace
 
 // Halo-tiled predicate: 64-channel groups and a tile whose receptive field
-// fits the LDS stage.  Any filter size, stride and dilation.
+// fits LDS.  Any filter size, stride and dilation.  3x3 layers whose halo of
+// all channel groups fits LDS use the resident-halo kernel (input read once
+// per tile, filter streamed); the others stage one channel group at a time.
 bool plan_halo(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
   if (s.c % 64 != 0) return false;
-  return search_patch_plan(s, g, false, p);
+  const int bn = s.k > 64 ? 128 : 64;
+  if (plan_resident(s, g, p))
+    return true;
+  return search_patch_plan(s, g, PatchMode::kStagedHalo, bn, p);
 }
 
 // Spatial-strip predicate, re-derived from spatial_strip.cuh:11-15 for the
@@ -201,7 +261,7 @@ bool plan_strip(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
   if (!(s.r == 3 && s.s == 3 && s.stride_w == 1 && s.dilation_w == 1 &&
         s.c % 64 == 0))
     return false;
-  return search_patch_plan(s, g, true, p);
+  return search_patch_plan(s, g, PatchMode::kStrip, s.k > 64 ? 128 : 64, p);
 }
 
 ConvArgs make_args(const i8conv_shape &s, const i8conv_geometry &g,
