@@ -91,6 +91,49 @@ __device__ __forceinline__ v4i load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor as four dwords (same fields as make_rsrc), for the
+// inline-asm copy below.
+__device__ __forceinline__ v4u make_desc(const void *base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  return v4u{uint32_t(b), uint32_t(b >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return uint32_t(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const void *)p));
+}
+
+// One wave-wide 16-byte-per-lane copy from a buffer into LDS: lane i's 16
+// bytes at buffer offset `voffset` land at LDS address lds_base + 16*i
+// (zeros when voffset is out of range).  Issued as inline asm so that the
+// compiler does not model it: it would otherwise wait for every copy in
+// flight before any later LDS read.  The caller owns the vmcnt accounting
+// (these copies complete in issue order with the wave's other vector
+// memory loads).  M0 is set here and used by nothing else in these kernels.
+__device__ __forceinline__ void lds_copy16(v4u desc, uint32_t lds_base, uint32_t voffset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voffset), "s"(desc)
+      : "memory");
+}
+
+// Four consecutive int32 from `base` (bias), element e at index i0 + e,
+// zero where i0 + e >= count; no branches.
+__device__ __forceinline__ v4i load_bias4(const int32_t *base, int count, int i0) {
+  const auto r = make_rsrc(base, uint32_t(count) * 4u);
+  v4i v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    v[e] = __builtin_amdgcn_raw_buffer_load_b32(r, uint32_t(i0 + e) * 4u, 0, 0);
+  return v;
+}
+
 // D = A x B + C over int8 -> int32.  A is 16 rows (lane % 16) by 64 k,
 // B is 64 k by 16 columns (lane % 16); lane l supplies 16 k-bytes of its
 // row/column for k-block l / 16.  Any mapping of the 64 k positions onto

@@ -53,6 +53,7 @@ struct PatchPlan {
   bool resident = false;
   int ranges = 0;  // resident: pixel ranges per channel slice
   int copies = 0;  // resident: 1 KB LDS copies per wave per channel group
+  int ring = 0;    // resident: filter staging slots in LDS
 };
 bool plan_halo(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p);
 bool plan_strip(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p);
@@ -73,5 +74,12 @@ int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
 // Whether kernel_halo.hip has an instance for 16*fn channels per wave and
 // `steps` 64-byte k-steps.
 bool halo_instance_exists(int fn, int steps);
+// kernel_halo.hip stages the filter through a ring of up to kHaloRing LDS
+// slots of 64*fn rows x 128 bytes each, after the input rows.
+constexpr int kHaloRing = 8;
+inline size_t halo_ring_slot_bytes(int fn) { return size_t(64) * fn * 128; }
+// 1 KB copy instructions per wave to stage `pixels` input pixels of
+// `channels` channels (c + 16 LDS bytes per pixel) in kernel_halo.hip.
+size_t halo_input_copies(int pixels, int channels);
 
 }  // namespace i8conv

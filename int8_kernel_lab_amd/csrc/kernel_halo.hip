@@ -13,28 +13,34 @@
 // of all images consecutively.  A range needs the virtual rows from its
 // first pixel's tap-0 row to its last pixel's last-tap row; those rows (all
 // w + 2*pad_w columns, every 64-channel group) are copied into LDS once by
-// the buffer unit (buffer_load_dwordx4 ... lds, 1 KB per wave instruction).
-// Padding rows/columns and rows between images come back as zeros because
-// their buffer offsets are out of range.  LDS layout: [group][row][col][64 B]
-// with chunk j of pixel slot p at 16*(j ^ ((p >> 2) & 3)) (swz64).
+// the buffer unit (1 KB per wave instruction, whole pixels, so every copy
+// reads whole cache lines).  Padding rows/columns and rows between images
+// come back as zeros because their buffer offsets are out of range.  LDS
+// layout: [pixel][c + 16 bytes]: all channels of a pixel, then 16 bytes of
+// padding.  The pitch is an odd number of 16-byte units (c % 32 == 0), so
+// the 16 pixels of an MFMA fragment hit 16 different 16-byte bank groups of
+// the 64 x 4-byte LDS banks, and a fragment address is linear in the tap
+// offset: the k loop spends one add per fragment per step on addressing.
 //
-// Filter.  Each of the 4 waves owns 16*FN output channels and loads its
-// whole filter slice (16*FN x r*s*c bytes, kSteps 64-byte k-steps) into
-// VGPRs in k order; the k loop consumes step t as soon as its registers
-// land (the loads complete in issue order), so the fetch overlaps the first
-// pass's MFMAs.
+// Filter.  Each of the 4 waves owns 16*FN output channels and keeps its
+// whole filter slice (16*FN x r*s*c bytes, kSteps 64-byte k-steps) in VGPRs
+// for the life of the workgroup.  A fragment read straight from KRSC touches
+// 16 rows x 64 bytes (16 half-used cache lines) and streams at a third of
+// the rate of whole-line reads, so the slice is fetched with whole-line
+// copies (8 rows x 128 bytes per instruction) into an LDS ring of up to 8
+// slots (swz128 layout) and picked out of LDS in fragment order.  The first
+// pass consumes each 128-byte chunk as soon as it lands, so the filter fetch
+// overlaps that pass's MFMAs.
 //
-// Compute.  Fragments run four at a time through all k-steps (B fragments
-// read from LDS one step ahead), then get the bias and are stored; the next
-// pass computes while those stores drain.
+// Compute.  Fragments run up to four at a time through all k-steps (B
+// fragments read from LDS one step ahead), then get the bias and are stored;
+// the next pass computes while those stores drain.
 #include <hip/hip_runtime.h>
 
 #include "i8conv_internal.hpp"
 
 namespace i8conv {
 namespace {
-
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ v4i add_wrap(v4i a, v4i b) {
   return __builtin_bit_cast(v4i, __builtin_bit_cast(v4u, a) +
@@ -46,27 +52,16 @@ constexpr int kPassFrags = 4;
 struct HaloArgs {
   int wp;            // padded row width: w + 2*pad_w
   int hp;            // padded rows per image: h + 2*pad_h
-  int groups;        // c / 64
-  int group_bytes;   // LDS bytes per channel group (whole 4 KB copy rounds)
-  int copies;        // buffer->LDS instructions per wave per group
+  int pitch;         // LDS bytes per input pixel: c + 16
+  int units;         // 16-byte units per pixel in LDS: c / 16 + 1
+  int input_bytes;   // LDS bytes of the input rows (whole 4 KB copy rounds)
+  int copies;        // buffer->LDS instructions per wave for the input rows
   int ranges;        // pixel ranges per channel slice
+  int ring;          // filter staging slots in LDS (1..kHaloRing)
   int total_frags;   // ceil(M / 16)
   int tiles_n;
-  FastDiv div_ohw, div_ow, div_wp, div_hp;
+  FastDiv div_ohw, div_ow, div_wp, div_hp, div_units;
 };
-
-// k-step t (64 k-bytes) -> LDS pixel-slot offset of its tap and the byte
-// offset of its channel group.
-__device__ __forceinline__ void step_geometry(const ConvArgs &a, const HaloArgs &p,
-                                              int t, int &delta, int &gbase) {
-  const int k0 = t * 64;
-  const int tap = int(fast_div(uint32_t(k0), a.div_c));
-  const int g = (k0 - tap * a.c) >> 6;
-  const int fy = int(fast_div(uint32_t(tap), a.div_s));
-  const int fx = tap - fy * a.s;
-  delta = fy * a.dil_h * p.wp + fx * a.dil_w;
-  gbase = g * p.group_bytes;
-}
 
 // Virtual padded row of output pixel m's tap-0 row; also returns its column.
 __device__ __forceinline__ int pixel_vrow(const ConvArgs &a, const HaloArgs &p, int m, int &ox) {
@@ -77,14 +72,91 @@ __device__ __forceinline__ int pixel_vrow(const ConvArgs &a, const HaloArgs &p, 
   return b * p.hp + oy * a.stride_h;
 }
 
-// NF fragments starting at f0 through all k-steps, then bias + stores.
-template <int FN, int kSteps, int NF>
+// LDS byte offset of k-step t (64 k-bytes): its tap's pixel offset plus its
+// 64-channel group inside the pixel.  Wave-uniform.
+__device__ __forceinline__ int step_offset(const ConvArgs &a, const HaloArgs &p, int t) {
+  const int k0 = t * 64;
+  const int tap = int(fast_div(uint32_t(k0), a.div_c));
+  const int c0 = k0 - tap * a.c;
+  const int fy = int(fast_div(uint32_t(tap), a.div_s));
+  const int fx = tap - fy * a.s;
+  return (fy * a.dil_h * p.wp + fx * a.dil_w) * p.pitch + c0;
+}
+
+// The filter staging ring: chunk c = bytes [128c, 128c + 128) of the
+// workgroup's 64*FN filter rows.
+template <int FN, int kSteps>
+struct FilterRing {
+  static constexpr int kRows = 64 * FN;
+  static constexpr int kChunks = (kSteps + 1) / 2;
+  static constexpr int kChunkBytes = kRows * 128;
+  static constexpr int kCopies = kRows * 8 / 64 / 4;  // per wave per chunk
+  v4u wd;
+  uint32_t lds;  // LDS address of slot 0
+  const int8_t *ptr;
+  int slots, tile_n, wave, lane, gemm_k, gemm_n;
+
+  __device__ __forceinline__ void issue(int c) const {
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j) {
+      const int inst = wave + 4 * j;
+      const int slot = inst * 64 + lane;
+      const int r = slot >> 3;
+      const int chunk16 = (slot & 7) ^ (r & 7) ^ ((r >> 3) & 1);  // inverse of swz128
+      const int oc = tile_n + r;
+      const int k = c * 128 + chunk16 * 16;
+      const uint32_t off = oc < gemm_n && k < gemm_k ? uint32_t(oc * gemm_k + k) : kOutOfRange;
+      lds_copy16(wd, lds + (c % slots) * kChunkBytes + inst * 1024, off);
+    }
+  }
+  // Chunk c has landed once no more than `after` later chunks are
+  // outstanding: copies return in issue order, and everything issued before
+  // the ring (bias, input rows) is older than every chunk.
+  __device__ __forceinline__ void wait(int c) const {
+    const int after = min(slots - 1, kChunks - 1 - c);
+    switch (after) {
+      case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+      case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 * kCopies) : "memory"); break;
+      case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kCopies) : "memory"); break;
+      case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kCopies) : "memory"); break;
+      case 4: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kCopies) : "memory"); break;
+      case 5: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * kCopies) : "memory"); break;
+      case 6: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * kCopies) : "memory"); break;
+      default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(7 * kCopies) : "memory"); break;
+    }
+  }
+  // Waits for chunk c, moves its two k-steps into this wave's fragments and
+  // refills its slot with chunk c + slots.
+  __device__ __forceinline__ void take(int c, v4i (&wf)[kSteps][FN]) const {
+    wait(c);
+    __syncthreads();
+    const int8_t *src = ptr + (c % slots) * kChunkBytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = 2 * c + h;
+      if (t >= kSteps) break;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+        wf[t][i] = *reinterpret_cast<const v4i *>(
+            src + swz128(wave * 16 * FN + i * 16 + (lane & 15), 4 * h + (lane >> 4)));
+    }
+    if (c + slots < kChunks) {
+      __syncthreads();  // every wave has read this slot
+      issue(c + slots);
+    }
+  }
+};
+
+// NF fragments starting at f0 through all k-steps, then bias + stores.  The
+// staging pass (kStage) also pulls the filter out of the ring, chunk by chunk,
+// just before the steps that need it.
+template <int FN, int kSteps, int NF, bool kStage>
 __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
-                                          const int8_t *smem, const v4i (&wf)[kSteps][FN],
-                                          const v4i (&bv)[FN], int f0, int vr0, int m_first,
+                                          const int8_t *smem, const FilterRing<FN, kSteps> &ring,
+                                          v4i (&wf)[kSteps][FN], const v4i (&bv)[FN],
+                                          const int (&soff)[kSteps], int f0, int vr0, int m_first,
                                           int tile_n, int wave, int lane) {
-  const int chunk = lane >> 4;
-  int lbase[NF];
+  int vaddr[NF];
   int mpx[NF];
 #pragma unroll
   for (int j = 0; j < NF; ++j) {
@@ -93,7 +165,7 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
     if (mpx[j] < 0) m = m_first;  // past the last pixel: computed, never stored
     int ox;
     const int vr = pixel_vrow(a, p, m, ox);
-    lbase[j] = (vr - vr0) * p.wp + ox * a.stride_w;
+    vaddr[j] = ((vr - vr0) * p.wp + ox * a.stride_w) * p.pitch + 16 * (lane >> 4);
   }
   v4i acc[NF][FN];
 #pragma unroll
@@ -102,19 +174,19 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
     for (int i = 0; i < FN; ++i) acc[j][i] = v4i{0, 0, 0, 0};
 
   v4i bcur[NF], bnxt[NF];
-  int delta, gbase;
-  step_geometry(a, p, 0, delta, gbase);
 #pragma unroll
-  for (int j = 0; j < NF; ++j)
-    bcur[j] = *reinterpret_cast<const v4i *>(smem + gbase + swz64(lbase[j] + delta, chunk));
+  for (int j = 0; j < NF; ++j) bcur[j] = *reinterpret_cast<const v4i *>(smem + vaddr[j] + soff[0]);
 #pragma unroll
   for (int t = 0; t < kSteps; ++t) {
+    if (kStage && (t & 1) == 0) ring.take(t >> 1, wf);
     if (t + 1 < kSteps) {  // next step's B fragments, one step ahead of use
-      step_geometry(a, p, t + 1, delta, gbase);
 #pragma unroll
       for (int j = 0; j < NF; ++j)
-        bnxt[j] = *reinterpret_cast<const v4i *>(smem + gbase + swz64(lbase[j] + delta, chunk));
+        bnxt[j] = *reinterpret_cast<const v4i *>(smem + vaddr[j] + soff[t + 1]);
     }
+    // keep those reads ahead of this step's MFMAs (the scheduler would
+    // otherwise sink each read next to its use and expose the LDS latency)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NF; ++j)
 #pragma unroll
@@ -159,74 +231,76 @@ __global__ __launch_bounds__(kThreads, 1) void halo_kernel(ConvArgs a, HaloArgs 
   const int f_end = int((int64_t(range + 1) * p.total_frags) / p.ranges);
   const int tile_n = tn * 64 * FN;
 
-  const auto xr = make_rsrc(a.x, a.x_bytes);
-  const auto wr = make_rsrc(a.w, a.w_bytes);
+  // bias of this lane's four channels per fragment (issued first: every
+  // later wait on the copies also covers these loads)
+  v4i bv[FN];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+    bv[i] = load_bias4(a.bias, a.gemm_n, tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4));
 
+  const v4u xd = make_desc(a.x, a.x_bytes);
+  const uint32_t lds0 = lds_addr(smem);
   int ox_unused;
   const int m_first = f_begin * 16;
   const int m_last = min(f_end * 16, a.gemm_m) - 1;
   const int vr0 = pixel_vrow(a, p, m_first, ox_unused);
   const int vr1 = pixel_vrow(a, p, m_last, ox_unused) + (a.r - 1) * a.dil_h;
-  const int slots = (vr1 - vr0 + 1) * p.wp;  // LDS pixel slots per group
+  const int pixels = (vr1 - vr0 + 1) * p.wp;  // input pixels of the range
 
-  // ---- 1. input rows -> LDS (every channel group) -------------------------
-  for (int g = 0; g < p.groups; ++g) {
-    for (int j = 0; j < p.copies; ++j) {
-      const int inst = wave + 4 * j;
-      const int slot = inst * 64 + lane;
-      const int pix = slot >> 2;
-      uint32_t off = kOutOfRange;
-      if (pix < slots) {
-        const int rr = int(fast_div(uint32_t(pix), p.div_wp));
-        const int px = pix - rr * p.wp - a.pad_w;
-        const int vr = vr0 + rr;
-        const int b = int(fast_div(uint32_t(vr), p.div_hp));  // vr / hp
-        const int iy = vr - b * p.hp - a.pad_h;
-        if (b < a.n && unsigned(iy) < unsigned(a.h) && unsigned(px) < unsigned(a.wd))
-          off = uint32_t(((b * a.h + iy) * a.wd + px) * a.c + g * 64 +
-                         swz64_chunk(pix, slot & 3) * 16);
-      }
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xr, (__attribute__((address_space(3))) void *)(smem + g * p.group_bytes + inst * 1024),
-          16, off, 0, 0, 0);
+  // ---- 1. input rows (whole pixels) -> LDS ----------------------------------
+  for (int j = 0; j < p.copies; ++j) {
+    const int inst = wave + 4 * j;
+    const int slot = inst * 64 + lane;  // 16-byte unit; `units` per pixel
+    const int pix = int(fast_div(uint32_t(slot), p.div_units));
+    const int u = slot - pix * p.units;
+    uint32_t off = kOutOfRange;
+    if (u < p.units - 1 && pix < pixels) {
+      const int rr = int(fast_div(uint32_t(pix), p.div_wp));
+      const int px = pix - rr * p.wp - a.pad_w;
+      const int vr = vr0 + rr;
+      const int b = int(fast_div(uint32_t(vr), p.div_hp));
+      const int iy = vr - b * p.hp - a.pad_h;
+      if (b < a.n && unsigned(iy) < unsigned(a.h) && unsigned(px) < unsigned(a.wd))
+        off = uint32_t(((b * a.h + iy) * a.wd + px) * a.c + u * 16);
     }
+    lds_copy16(xd, lds0 + inst * 1024, off);
   }
 
-  asm volatile("" ::: "memory");  // keep every copy ahead of the filter loads
+  // ---- 2. start the filter ring --------------------------------------------
+  FilterRing<FN, kSteps> ring;
+  ring.wd = make_desc(a.w, a.w_bytes);
+  ring.ptr = smem + p.input_bytes;
+  ring.lds = lds_addr(ring.ptr);
+  ring.slots = p.ring;
+  ring.tile_n = tile_n;
+  ring.wave = wave;
+  ring.lane = lane;
+  ring.gemm_k = a.gemm_k;
+  ring.gemm_n = a.gemm_n;
+  for (int c = 0; c < ring.slots && c < ring.kChunks; ++c) ring.issue(c);
 
-  // ---- 2. this wave's filter slice -> VGPRs, in k order ---------------------
+  // ---- 3. passes of up to four fragments -------------------------------------
+  int soff[kSteps];
+#pragma unroll
+  for (int t = 0; t < kSteps; ++t) soff[t] = step_offset(a, p, t);
   v4i wf[kSteps][FN];
-#pragma unroll
-  for (int i = 0; i < FN; ++i) {
-    const int oc = tile_n + wave * 16 * FN + i * 16 + (lane & 15);
-    const int row = oc < a.gemm_n ? oc * a.gemm_k + 16 * (lane >> 4) : -1;
-#pragma unroll
-    for (int t = 0; t < kSteps; ++t)
-      wf[t][i] = load16(wr, row >= 0 ? uint32_t(row + t * 64) : kOutOfRange);
+  int f0 = f_begin;
+  {
+    const int nf = min(kPassFrags, f_end - f0);
+    switch (nf) {
+      case 4: halo_pass<FN, kSteps, 4, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 3: halo_pass<FN, kSteps, 3, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 2: halo_pass<FN, kSteps, 2, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      default: halo_pass<FN, kSteps, 1, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+    }
+    f0 += nf;
   }
-  // The input rows are complete once every load issued before the filter
-  // and bias loads has returned (loads return in order).
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kSteps * FN) : "memory");
-  __syncthreads();
-  v4i bv[FN];
-#pragma unroll
-  for (int i = 0; i < FN; ++i) {
-    const int oc0 = tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4);
-    bv[i] = v4i{0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (oc0 + e < a.gemm_n) bv[i][e] = a.bias[oc0 + e];
-  }
-
-
-
-  // ---- 3. passes of up to four fragments ------------------------------------
-  for (int f0 = f_begin; f0 < f_end; f0 += kPassFrags) {
+  for (; f0 < f_end; f0 += kPassFrags) {
     switch (min(kPassFrags, f_end - f0)) {
-      case 4: halo_pass<FN, kSteps, 4>(a, p, smem, wf, bv, f0, vr0, m_first, tile_n, wave, lane); break;
-      case 3: halo_pass<FN, kSteps, 3>(a, p, smem, wf, bv, f0, vr0, m_first, tile_n, wave, lane); break;
-      case 2: halo_pass<FN, kSteps, 2>(a, p, smem, wf, bv, f0, vr0, m_first, tile_n, wave, lane); break;
-      default: halo_pass<FN, kSteps, 1>(a, p, smem, wf, bv, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 4: halo_pass<FN, kSteps, 4, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 3: halo_pass<FN, kSteps, 3, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 2: halo_pass<FN, kSteps, 2, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      default: halo_pass<FN, kSteps, 1, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
     }
   }
 }
@@ -259,26 +333,36 @@ bool halo_instance_exists(int fn, int steps) {
          (fn == 2 && (steps == 9 || steps == 18));
 }
 
+size_t halo_input_copies(int pixels, int channels) {
+  // (c/16 + 1) 16-byte units per pixel; 4 waves x 64 units per round
+  return (size_t(pixels) * size_t(channels / 16 + 1) + 255) / 256;
+}
+
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream) {
   HaloArgs h{};
   h.wp = a.wd + 2 * a.pad_w;
   h.hp = a.h + 2 * a.pad_h;
-  h.groups = a.c / 64;
+  h.pitch = a.c + 16;
+  h.units = a.c / 16 + 1;
   h.copies = p.copies;
-  h.group_bytes = p.copies * 4 * 1024;
+  h.input_bytes = p.copies * 4 * 1024;
   h.ranges = p.ranges;
+  h.ring = p.ring;
   h.total_frags = (a.gemm_m + 15) / 16;
   h.tiles_n = p.tiles_n;
   h.div_ohw = make_fastdiv(uint32_t(a.out_h * a.out_w));
   h.div_ow = make_fastdiv(uint32_t(a.out_w));
   h.div_wp = make_fastdiv(uint32_t(h.wp));
   h.div_hp = make_fastdiv(uint32_t(h.hp));
-  const size_t lds = size_t(h.groups) * h.group_bytes;
-  const size_t blocks = size_t(p.ranges) * p.tiles_n;
+  h.div_units = make_fastdiv(uint32_t(h.units));
   const int fn = p.bn / 64;
+  const size_t lds = size_t(h.input_bytes) + size_t(p.ring) * halo_ring_slot_bytes(fn);
+  const size_t blocks = size_t(p.ranges) * p.tiles_n;
   const int steps = a.gemm_k / 64;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (a.c % 64 != 0 || !halo_instance_exists(fn, steps) || lds > size_t(kLdsBudget)) {
+  if (a.c % 64 != 0 || !halo_instance_exists(fn, steps) || lds > size_t(kLdsBudget) ||
+      a.c / 16 + 1 > 255 ||
+      p.ring < 1 || p.ring > kHaloRing) {
     set_error("halo plan out of range");
     return I8CONV_BAD_ARGUMENT;
   }

@@ -146,8 +146,13 @@ bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p
     const int64_t oy = (m % (int64_t(g.out_h) * g.out_w)) / g.out_w;
     return b * hp + oy * s.stride_h;
   };
-  for (int64_t ranges = std::max<int64_t>(1, std::min(total_frags, ceil_div(256, tiles_n)));
-       ranges <= total_frags; ranges = std::min(total_frags, ranges * 5 / 4 + 1)) {
+  const int64_t first = std::max<int64_t>(1, std::min(total_frags, ceil_div(256, tiles_n)));
+  const int64_t chunks = ceil_div(g.gemm_k, 128);
+  for (int64_t ranges = first; ranges <= total_frags;
+       ranges = std::min(total_frags, ranges * 5 / 4 + 1)) {
+    // each workgroup re-reads the whole filter slice: beyond the first grid
+    // that fills the compute units, keep at least four fragments per range
+    if (ranges > first && total_frags / ranges < 4) break;
     int64_t max_slots = 0;
     for (int64_t r = 0; r < ranges; ++r) {
       const int64_t f0 = r * total_frags / ranges, f1 = (r + 1) * total_frags / ranges;
@@ -156,9 +161,12 @@ bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p
       const int64_t rows = vrow(m1) - vrow(m0) + int64_t(s.r - 1) * s.dilation_h + 1;
       max_slots = std::max(max_slots, rows * wp);
     }
-    const int64_t copies = ceil_div(max_slots * 4, kThreads);  // 4 waves x 64 slots
-    const int64_t lds = int64_t(s.c / 64) * copies * 4096;
-    if (lds <= kLdsBudget && ranges * tiles_n <= INT32_MAX) {
+    const int64_t copies = int64_t(halo_input_copies(int(std::min<int64_t>(max_slots, INT32_MAX)), s.c));
+    const int64_t input_lds = copies * 4096;
+    const int64_t slot = int64_t(halo_ring_slot_bytes(fn));
+    const int64_t ring = std::min<int64_t>({kHaloRing, chunks, (kLdsBudget - input_lds) / slot});
+    if (ring >= 1 && ranges * tiles_n <= INT32_MAX) {
+      p->ring = int(ring);
       p->resident = true;
       p->strip = false;
       p->bn = 64 * fn;
