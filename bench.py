@@ -46,6 +46,62 @@ def cpu_baseline(shape, x, w, b, threads: int, min_cpu_seconds: float = 10.0):
                       f"({reps * shape.ops() / 1e9:.1f} GOP, {t_total:.2f} s wall)"}
 
 
+def copy_calibration(mib: int, steps: int) -> int:
+    """A kernel of known HBM traffic: y = -x over MIB MiB of int32, with x and
+    y distinct buffers far larger than the L2 and the MALL, so each launch
+    reads and writes exactly MIB MiB of HBM."""
+    import torch
+    n = mib * (1 << 20) // 4
+    x = torch.ones(n, dtype=torch.int32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(steps):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    assert int(y[0]) == -1 and int(y[-1]) == -1
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
+                      "launches": steps}), flush=True)
+    return 0
+
+
+def write_floor(workload: str, steps: int, warmup: int) -> int:
+    """Times torch's fill kernel over exactly the layer's output bytes (the
+    NHWK int32 tensor every candidate must store), back to back between two
+    events on the current stream: no convolution can finish faster."""
+    import torch
+    import int8_kernel_lab_amd as lab
+    shape = lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), workload)
+    y = torch.empty(shape.geometry().output_elements, dtype=torch.int32, device="cuda")
+    for _ in range(warmup):
+        y.fill_(7)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        y.fill_(7)
+    stop.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / steps
+    print(json.dumps({"write_floor_workload": workload, "bytes": y.numel() * 4,
+                      "us_per_launch": round(us, 3),
+                      "tops_if_conv_took_this_long": round(shape.ops() / (us * 1e-6) / 1e12, 1),
+                      "launches": steps}), flush=True)
+    return 0
+
+
+def traffic_record(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.json),
+    scaled by the same counters' reading for the copy kernel; None when that
+    pair was not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        table = json.load(f)
+    rec = table.get("kernels", {}).get(f"{workload}/{kernel}")
+    return None if rec is None else int(rec["traffic_bytes"])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -55,7 +111,18 @@ def main() -> int:
                     help="dispatch (default) or one of generic|strip|halo|splitk")
     ap.add_argument("--workload", default=WORKLOAD)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run a plain device copy of MIB MiB "
+                         "(int32 negate: reads and writes MIB MiB) --steps times, to scale "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
+    ap.add_argument("--write-floor", action="store_true",
+                    help="instead of the benchmark, time a plain fill kernel writing exactly "
+                         "the workload's int32 output bytes (the store traffic alone)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration, args.steps)
+    if args.write_floor:
+        return write_floor(args.workload, args.steps, args.warmup)
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this lab measures one GPU "
               "(each box has one MI355X; the layer is not sharded across GPUs)", file=sys.stderr)
@@ -131,7 +198,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / PEAK_HBM_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic_record(args.workload, kernel),
         },
         "cpu_baseline": cpu,
     }

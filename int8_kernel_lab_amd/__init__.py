@@ -34,7 +34,8 @@ __all__ = [
     "eligible", "fill_int8", "fill_int32", "kernel_names", "launch",
     "launch_generic", "launch_spatial_strip", "load_case", "load_workloads",
     "make_case_data", "measure", "spatial_strip_eligible", "workspace_bytes",
-    "WORKLOADS_DIR", "BASELINE_SEED", "device_info", "synchronize",
+    "WORKLOADS_DIR", "BASELINE_SEED", "device_count", "device_info", "set_device",
+    "synchronize",
 ]
 
 KERNELS = ("generic", "strip", "halo", "splitk")
@@ -267,6 +268,18 @@ def launch_spatial_strip(shape: ConvShape, input, filter, bias, output, stream=N
 
 def synchronize() -> None:
     check(lib().i8conv_synchronize(), "synchronize")
+
+
+def device_count() -> int:
+    n = ctypes.c_int()
+    check(lib().i8conv_device_count(ctypes.byref(n)), "device count")
+    return n.value
+
+
+def set_device(index: int) -> None:
+    """Makes GPU `index` current for the calling thread (buffers and launches
+    that follow use it)."""
+    check(lib().i8conv_set_device(int(index)), f"set device {index}")
 
 
 def measure(name: str, shape: ConvShape, input, filter, bias, output, workspace=None,

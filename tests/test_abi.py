@@ -1,0 +1,239 @@
+"""CPU tests of the C ABI (include/i8conv.h): exports, status codes, shape
+derivation, eligibility predicates, dispatch policy and launch-argument
+errors.  Nothing here launches a kernel: every launch call below fails its
+argument checks before the library touches HIP.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import int8_kernel_lab_amd as lab
+from int8_kernel_lab_amd import _lib
+from oracle import oracle
+from tests.golden.make_golden import out_extent
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "i8conv.h")
+REFERENCE_TABLE = os.path.join(lab.WORKLOADS_DIR, "reference.csv")
+BASELINE_TABLE = os.path.join(lab.WORKLOADS_DIR, "baseline.csv")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(i8conv_\w+)\s*\(", text)))
+
+
+def all_shapes():
+    shapes = dict(lab.load_workloads(REFERENCE_TABLE))
+    shapes.update(lab.load_workloads(BASELINE_TABLE))
+    return shapes
+
+
+# ---- exports ---------------------------------------------------------------
+
+def test_library_exports_every_declared_function():
+    names = header_functions()
+    assert len(names) >= 30
+    handle = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in names if not hasattr(handle, n)]
+    assert not missing, f"declared in i8conv.h but not exported: {missing}"
+
+
+def test_python_binding_covers_exactly_the_header():
+    assert sorted(_lib.SIGNATURES) == header_functions()
+
+
+def test_status_strings():
+    expected = {_lib.OK: "ok", _lib.INELIGIBLE: "ineligible", _lib.BAD_SHAPE: "bad shape",
+                _lib.BAD_ARGUMENT: "bad argument",
+                _lib.WORKSPACE_TOO_SMALL: "workspace too small",
+                _lib.HIP_ERROR: "hip error", _lib.UNKNOWN_KERNEL: "unknown kernel"}
+    for code, text in expected.items():
+        assert text in _lib.lib().i8conv_status_string(code).decode()
+    assert _lib.lib().i8conv_status_string(99)
+
+
+def test_kernel_registry():
+    assert lab.kernel_names() == lab.KERNELS
+    for i, name in enumerate(lab.KERNELS):
+        assert _lib.lib().i8conv_kernel_id(name.encode()) == i
+    assert _lib.lib().i8conv_kernel_id(b"cudnn") == -1
+    assert _lib.lib().i8conv_kernel_name(4) is None
+    assert _lib.lib().i8conv_kernel_name(-1) is None
+
+
+# ---- shape derivation (conv_shape.cuh:22-35) --------------------------------
+
+def test_reference_workload_table_is_complete():
+    shapes = lab.load_workloads(REFERENCE_TABLE)
+    assert len(shapes) == 41
+    assert "big_3x3_s1" in shapes and "smoke" in shapes
+
+
+@pytest.mark.parametrize("name,shape", sorted(all_shapes().items()), ids=lambda v: str(v))
+def test_derive_matches_closed_form_and_oracle(name, shape):
+    g = shape.geometry()
+    oh = out_extent(shape.h, shape.pad_h, shape.dilation_h, shape.r, shape.stride_h)
+    ow = out_extent(shape.w, shape.pad_w, shape.dilation_w, shape.s, shape.stride_w)
+    assert (g.out_h, g.out_w) == (oh, ow)
+    assert g.gemm_m == shape.n * oh * ow
+    assert g.gemm_n == shape.k
+    assert g.gemm_k == shape.r * shape.s * shape.c
+    assert g.input_elements == shape.n * shape.h * shape.w * shape.c
+    assert g.filter_elements == shape.k * shape.r * shape.s * shape.c
+    assert g.output_elements == g.gemm_m * shape.k
+    og = oracle.derive(shape)
+    assert (og.out_h, og.out_w, og.gemm_m, og.gemm_k) == (g.out_h, g.out_w, g.gemm_m, g.gemm_k)
+
+
+@pytest.mark.parametrize("shape,reason", [
+    (lab.ConvShape(1, 8, 8, 24, 8, 3, 3, 1, 1), "divisible by 16"),      # conv_shape.cuh:34
+    (lab.ConvShape(1, 2, 2, 16, 8, 5, 5, 0, 0), "nonempty"),             # conv_shape.cuh:35
+    (lab.ConvShape(1, 8, 8, 16, 8, 3, 3, 1, 1, 0, 1), "out of range"),   # stride 0
+    (lab.ConvShape(0, 8, 8, 16, 8, 3, 3), "out of range"),
+    (lab.ConvShape(1, 8, 8, 16, 8, 3, 3, -1, 0), "out of range"),
+    (lab.ConvShape(1, 8, 8, 16, 8, 3, 3, 1, 1, 1, 1, 0, 1), "out of range"),
+    (lab.ConvShape(1, 65536, 65536, 16, 8, 1, 1), "too large"),          # 2^36 input bytes
+])
+def test_bad_shapes_are_rejected(shape, reason):
+    g = _lib.CGeometry()
+    assert _lib.lib().i8conv_derive(ctypes.byref(shape.c_struct()), ctypes.byref(g)) == _lib.BAD_SHAPE
+    assert reason in _lib.lib().i8conv_last_error().decode()
+    with pytest.raises(ValueError):
+        shape.geometry()
+    for name in lab.KERNELS:
+        assert not lab.eligible(name, shape)
+    assert _lib.lib().i8conv_dispatch(ctypes.byref(shape.c_struct())) == -1
+
+
+def test_truncating_output_formula_is_kept():
+    # (2 + 0 - 2 - 1) / 2 + 1 = 1 in C (truncation toward zero), 0 with floor
+    shape = lab.ConvShape(1, 2, 2, 16, 8, 3, 3, 0, 0, 2, 2, 1, 1)
+    assert (shape.out_h, shape.out_w) == (1, 1)
+
+
+# ---- eligibility predicates --------------------------------------------------
+
+def test_reference_strip_predicate_selects_only_big_3x3_s1():
+    # spatial_strip.cuh:11-15 over the reference's own table
+    chosen = [n for n, s in lab.load_workloads(REFERENCE_TABLE).items()
+              if oracle.strip_eligible_reference(s)]
+    assert chosen == ["big_3x3_s1"]
+
+
+@pytest.mark.parametrize("name,shape", sorted(all_shapes().items()), ids=lambda v: str(v))
+def test_gfx950_strip_predicate_closed_form(name, shape):
+    # the gfx950 strip tile keeps the reference's 3x3 / unit horizontal
+    # stride and dilation / C % 64 conditions and drops K % 64 and
+    # out_w % 128 (it tiles whole output rows and masks channel tails)
+    want = (shape.r == 3 and shape.s == 3 and shape.stride_w == 1 and
+            shape.dilation_w == 1 and shape.c % 64 == 0)
+    assert lab.spatial_strip_eligible(shape) == want
+    assert lab.eligible("strip", shape) == want
+    # every shape the reference's predicate admits stays eligible
+    if oracle.strip_eligible_reference(shape):
+        assert want
+
+
+@pytest.mark.parametrize("name,shape", sorted(all_shapes().items()), ids=lambda v: str(v))
+def test_generic_and_halo_predicates(name, shape):
+    assert lab.eligible("generic", shape)
+    assert lab.eligible("halo", shape) == (shape.c % 64 == 0)
+    assert lab.eligible("splitk", shape) == (shape.geometry().gemm_k > 128)
+
+
+BASELINE_TABLE_EXPECTED = {
+    # name: (strip, halo, dispatch)
+    "cfg1_smoke": (True, True, "halo"),
+    "cfg2_resnet_3x3_s1": (True, True, "halo"),
+    "cfg3_down_3x3_s2": (False, True, "halo"),
+    "cfg4a_pointwise_1x1": (False, True, "generic"),
+    "cfg4b_k36_tail": (True, True, "halo"),
+    "cfg5a_deep_k": (True, True, "splitk"),
+    "cfg5b_dilated": (False, True, "halo"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(BASELINE_TABLE_EXPECTED))
+def test_baseline_eligibility_and_dispatch(name, baseline_cases):
+    shape = baseline_cases[name]
+    strip, halo, chosen = BASELINE_TABLE_EXPECTED[name]
+    assert lab.eligible("strip", shape) == strip
+    assert lab.eligible("halo", shape) == halo
+    assert lab.dispatch(shape) == chosen
+
+
+@pytest.mark.parametrize("name,shape", sorted(all_shapes().items()), ids=lambda v: str(v))
+def test_dispatch_returns_an_eligible_kernel_with_its_workspace(name, shape):
+    chosen = lab.dispatch(shape)
+    assert lab.eligible(chosen, shape)
+    s = shape.c_struct()
+    assert _lib.lib().i8conv_dispatch_workspace_bytes(ctypes.byref(s)) == \
+        lab.workspace_bytes(chosen, shape)
+    for name_ in ("generic", "strip", "halo"):
+        assert lab.workspace_bytes(name_, shape) == 0
+    if lab.eligible("splitk", shape):
+        g = shape.geometry()
+        ws = lab.workspace_bytes("splitk", shape)
+        # one int32 partial sum per output per split, at least two splits
+        assert ws % (4 * g.output_elements) == 0 and ws >= 8 * g.output_elements
+    assert lab.describe(chosen, shape).startswith(chosen)
+
+
+def test_describe_errors_and_truncation(baseline_cases):
+    shape = baseline_cases["cfg3_down_3x3_s2"]
+    buf = ctypes.create_string_buffer(8)
+    s = shape.c_struct()
+    L = _lib.lib()
+    assert L.i8conv_describe(1, ctypes.byref(s), buf, 8) == _lib.INELIGIBLE
+    assert L.i8conv_describe(7, ctypes.byref(s), buf, 8) == _lib.UNKNOWN_KERNEL
+    assert L.i8conv_describe(0, ctypes.byref(s), buf, 0) == _lib.BAD_ARGUMENT
+    assert L.i8conv_describe(0, ctypes.byref(s), buf, 8) == _lib.OK
+    assert buf.value == b"generic"  # 7 characters and the terminator
+
+
+# ---- launch argument errors (returned before any HIP call) ------------------
+
+FAKE = 0x10000  # a 64 KB-aligned address that is never dereferenced
+
+
+def _launch(kid, shape, x=FAKE, w=FAKE, b=FAKE, y=FAKE, ws=None, ws_n=0):
+    s = shape.c_struct() if shape is not None else None
+    return _lib.lib().i8conv_launch(kid, ctypes.byref(s) if s is not None else None,
+                                    x, w, b, y, ws, ws_n, None)
+
+
+def test_launch_errors_without_touching_the_gpu(baseline_cases):
+    cfg3 = baseline_cases["cfg3_down_3x3_s2"]
+    assert _launch(9, cfg3) == _lib.UNKNOWN_KERNEL
+    assert _launch(0, None) == _lib.BAD_ARGUMENT
+    assert _launch(0, lab.ConvShape(1, 8, 8, 24, 8, 3, 3, 1, 1)) == _lib.BAD_SHAPE
+    assert _launch(0, cfg3, x=None) == _lib.BAD_ARGUMENT
+    assert _launch(0, cfg3, y=None) == _lib.BAD_ARGUMENT
+    assert _launch(0, cfg3, x=FAKE + 8) == _lib.BAD_ARGUMENT   # input not 16-byte aligned
+    assert _launch(0, cfg3, w=FAKE + 4) == _lib.BAD_ARGUMENT   # filter not 16-byte aligned
+    assert _launch(0, cfg3, y=FAKE + 2) == _lib.BAD_ARGUMENT   # output not 4-byte aligned
+    assert _launch(1, cfg3) == _lib.INELIGIBLE                 # stride_w 2: no strip
+    assert "not eligible" in _lib.lib().i8conv_last_error().decode()
+    assert _launch(3, cfg3) == _lib.WORKSPACE_TOO_SMALL
+    need = lab.workspace_bytes("splitk", cfg3)
+    assert _launch(3, cfg3, ws=FAKE, ws_n=need - 1) == _lib.WORKSPACE_TOO_SMALL
+    assert _launch(3, cfg3, ws=FAKE + 4, ws_n=need) == _lib.WORKSPACE_TOO_SMALL
+    assert str(need) in _lib.lib().i8conv_last_error().decode()
+    shape = cfg3.c_struct()
+    assert _lib.lib().i8conv_launch_spatial_strip(ctypes.byref(shape), FAKE, FAKE, FAKE,
+                                                  FAKE, None) == _lib.INELIGIBLE
+    bad = lab.ConvShape(1, 8, 8, 24, 8, 3, 3, 1, 1).c_struct()
+    assert _lib.lib().i8conv_launch_dispatched(ctypes.byref(bad), FAKE, FAKE, FAKE, FAKE,
+                                               None, 0, None) == _lib.BAD_SHAPE
+
+
+def test_python_layer_raises_on_bad_calls(baseline_cases):
+    with pytest.raises(ValueError, match="unknown kernel"):
+        lab.eligible("cudnn", baseline_cases["cfg1_smoke"])
+    with pytest.raises(lab.I8ConvError, match="ineligible"):
+        lab.launch("strip", baseline_cases["cfg3_down_3x3_s2"], FAKE, FAKE, FAKE, FAKE)

@@ -4,10 +4,11 @@ import csv
 import io
 import os
 import subprocess
+import sys
 
 import pytest
 
-from tests.conftest import DRIVER, say
+from tests.conftest import DRIVER, ROOT, say
 
 REF_COLUMNS = ["case", "n", "h", "w", "c", "k", "r", "s", "out_h", "out_w", "eligible_strip",
                "generic_ms", "strip_ms", "winner", "generic_correct", "strip_correct"]
@@ -56,3 +57,20 @@ def test_driver_human_line_and_reference_value_range():
                    "--warmup", "1", "--iterations", "3")
     assert p.returncode == 0, p.stderr
     assert p.stdout.startswith("cfg4b_k36_tail:") and "winner" in p.stdout
+
+
+@pytest.mark.gpu
+def test_sweep_over_reference_cases(tmp_path):
+    # the sweep (sweep.py:10-62): one row per case, rewritten after each case
+    out = tmp_path / "sweep.csv"
+    say("[gpu] sweep over smoke,nonmultiple8_k63,batch8_asymmetric_1x3")
+    p = subprocess.run([sys.executable, "-m", "int8_kernel_lab_amd.sweep", "--cases",
+                        "smoke,nonmultiple8_k63,batch8_asymmetric_1x3", "--iterations", "3",
+                        "--warmup", "1", "--output", str(out)],
+                       capture_output=True, text=True, timeout=300, cwd=ROOT)
+    assert p.returncode == 0, p.stdout + p.stderr
+    rows = list(csv.DictReader(out.open()))
+    assert [r["case"] for r in rows] == ["smoke", "nonmultiple8_k63", "batch8_asymmetric_1x3"]
+    for r in rows:
+        assert r["generic_correct"] == "1" and r["winner"] != "none"
+        assert r["dispatch"] in ("generic", "strip", "halo", "splitk")

@@ -5,12 +5,21 @@ cannot pass on stale data), launches through the C ABI, and compares EVERY
 output element with oracle.conv (the restatement of conv_lab.cu:39-66).
 The reference checked 2048 sampled outputs (conv_lab.cu:72-77).
 """
+import hashlib
+import json
+import os
+
 import numpy as np
 import pytest
 
 import int8_kernel_lab_amd as lab
 from oracle import oracle
 from tests.conftest import say
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "baseline_outputs.json")
+with open(GOLDEN) as _f:
+    GOLDEN_CONFIGS = json.load(_f)["configs"]
 
 BASELINE_NAMES = ["cfg1_smoke", "cfg2_resnet_3x3_s1", "cfg3_down_3x3_s2",
                   "cfg4a_pointwise_1x1", "cfg4b_k36_tail", "cfg5a_deep_k", "cfg5b_dilated"]
@@ -92,6 +101,8 @@ def test_baseline_config_bit_exact(case, kernel, baseline_cases):
     say(f"[gpu] {kernel} on {case} {shape}")
     got = run_kernel(kernel, shape, x, w, b)
     assert_bit_exact(got, expected, f"{kernel}/{case}")
+    # and the torch-float64 golden hash of the full output (tests/golden)
+    assert hashlib.sha256(got.tobytes()).hexdigest() == GOLDEN_CONFIGS[case]["output_sha256"]
 
 
 @pytest.mark.gpu
@@ -134,6 +145,25 @@ def test_extreme_values_do_not_lose_bits():
             continue
         say(f"[gpu] {kernel} on extreme values")
         assert_bit_exact(run_kernel(kernel, shape, x, w, b), expected, f"{kernel}/extreme")
+
+
+@pytest.mark.gpu
+def test_int32_accumulator_wraps_like_the_oracle():
+    # 9 taps x 16384 channels x (-128 * -128) = 9 * 2^28 > 2^31 at the
+    # centre output: the int32 sum wraps in the oracle and on the MFMA alike
+    shape = lab.ConvShape(1, 3, 3, 16384, 8, 3, 3, 1, 1, 1, 1, 1, 1)
+    x = np.full((1, 3, 3, 16384), -128, np.int8)
+    w = np.full((8, 3, 3, 16384), -128, np.int8)
+    w[1] = 127  # products of -16256: a negative sum that does not wrap
+    b = np.arange(8, dtype=np.int32) * 1000 - 3000
+    expected = oracle.conv(shape, x, w, b)
+    exact = 9 * 16384 * 16384 - 3000
+    assert int(expected[0, 1, 1, 0]) == (exact + 2 ** 31) % 2 ** 32 - 2 ** 31
+    for kernel in lab.KERNELS:
+        if not lab.eligible(kernel, shape):
+            continue
+        say(f"[gpu] {kernel} on int32 wrap case")
+        assert_bit_exact(run_kernel(kernel, shape, x, w, b), expected, f"{kernel}/wrap")
 
 
 @pytest.mark.gpu
