@@ -99,7 +99,9 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
       d = std::string(kNames[id]) + " resident rows: " + std::to_string(p.ranges) +
           " pixel ranges of <=" + std::to_string(p.frags_m * 16) + "px x " +
           std::to_string(p.bn) + "oc, LDS " +
-          std::to_string(size_t(p.copies) * 4) + "+" +
+          std::to_string((kHaloBiasLds + size_t(p.rows) *
+                         size_t(halo_row_layout(shape->w + 2 * shape->pad_w, shape->c).row_bytes)) /
+                         1024) + "+" +
           std::to_string(p.ring * halo_ring_slot_bytes(p.bn / 64) / 1024) + " KB, grid " +
           std::to_string(int64_t(p.ranges) * p.tiles_n);
     } else {

@@ -123,6 +123,18 @@ __device__ __forceinline__ void lds_copy16(v4u desc, uint32_t lds_base, uint32_t
       : "memory");
 }
 
+// As lds_copy16 with 4 bytes per lane: lane i's dword at buffer offset
+// `voffset` lands at lds_base + 4*i (zero when out of range).
+__device__ __forceinline__ void lds_copy4(v4u desc, uint32_t lds_base, uint32_t voffset) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voffset), "s"(desc)
+      : "memory");
+}
+
 // Four consecutive int32 from `base` (bias), element e at index i0 + e,
 // zero where i0 + e >= count; no branches.
 __device__ __forceinline__ v4i load_bias4(const int32_t *base, int count, int i0) {

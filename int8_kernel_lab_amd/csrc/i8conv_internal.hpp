@@ -52,7 +52,7 @@ struct PatchPlan {
   // group resident in LDS and the filter slice in registers (kernel_halo.hip)
   bool resident = false;
   int ranges = 0;  // resident: pixel ranges per channel slice
-  int copies = 0;  // resident: 1 KB LDS copies per wave per channel group
+  int rows = 0;    // resident: most padded input rows any range needs
   int ring = 0;    // resident: filter staging slots in LDS
 };
 bool plan_halo(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p);
@@ -77,9 +77,27 @@ bool halo_instance_exists(int fn, int steps);
 // kernel_halo.hip stages the filter through a ring of up to kHaloRing LDS
 // slots of 64*fn rows x 128 bytes each, after the input rows.
 constexpr int kHaloRing = 8;
+// ... and keeps the bias of each wave's channels in the first kHaloBiasLds
+// bytes (256 per wave), before the input rows.
+constexpr int kHaloBiasLds = 1024;
 inline size_t halo_ring_slot_bytes(int fn) { return size_t(64) * fn * 128; }
-// 1 KB copy instructions per wave to stage `pixels` input pixels of
-// `channels` channels (c + 16 LDS bytes per pixel) in kernel_halo.hip.
-size_t halo_input_copies(int pixels, int channels);
+// LDS layout of one padded input row in kernel_halo.hip: wp pixels of
+// `units` 16-byte units each (all c channels, then one pad unit), written by
+// row_copies 1 KB copy instructions.  Rows are row_bytes apart, with
+// row_bytes / 16 >= 64 * row_copies (a row's copies never spill into the
+// next row) and row_bytes / 16 == row_units (mod 16), so the 16-byte bank
+// groups keep cycling across a row boundary as they do inside a row.
+struct HaloRowLayout {
+  int64_t units, row_units, row_copies, row_bytes;
+};
+inline HaloRowLayout halo_row_layout(int64_t wp, int64_t c) {
+  HaloRowLayout l;
+  l.units = c / 16 + 1;
+  l.row_units = wp * l.units;
+  l.row_copies = (l.row_units + 63) / 64;
+  const int64_t span = 64 * l.row_copies;
+  l.row_bytes = 16 * (span + ((l.row_units - span) % 16 + 16) % 16);
+  return l;
+}
 
 }  // namespace i8conv

@@ -13,14 +13,24 @@
 // of all images consecutively.  A range needs the virtual rows from its
 // first pixel's tap-0 row to its last pixel's last-tap row; those rows (all
 // w + 2*pad_w columns, every 64-channel group) are copied into LDS once by
-// the buffer unit (1 KB per wave instruction, whole pixels, so every copy
-// reads whole cache lines).  Padding rows/columns and rows between images
-// come back as zeros because their buffer offsets are out of range.  LDS
-// layout: [pixel][c + 16 bytes]: all channels of a pixel, then 16 bytes of
-// padding.  The pitch is an odd number of 16-byte units (c % 32 == 0), so
-// the 16 pixels of an MFMA fragment hit 16 different 16-byte bank groups of
-// the 64 x 4-byte LDS banks, and a fragment address is linear in the tap
-// offset: the k loop spends one add per fragment per step on addressing.
+// the buffer unit (1 KB per wave instruction).  Copies never straddle rows,
+// so everything about the row (image, input row, padding) is wave-uniform
+// scalar arithmetic and a lane only finds its pixel in the row.  Padding
+// rows/columns and rows between images come back as zeros because their
+// buffer offsets are out of range.  LDS layout: a row is [pixel][c + 16
+// bytes] (all channels of a pixel, then 16 bytes of padding), rows
+// row_bytes apart (HaloRowLayout).  The pixel pitch is an odd number of
+// 16-byte units (c % 32 == 0), so the 16 pixels of an MFMA fragment hit 16
+// different 16-byte bank groups of the 64 x 4-byte LDS banks, and a fragment
+// address is linear in the tap offset: the k loop spends one add per
+// fragment per step on addressing.
+//
+// Issue cost.  A wave64 VALU instruction takes at least 4 cycles and the
+// 32-bit multiplies 16, so per-copy address arithmetic is kept to a few
+// instructions: row math is scalar, filter copy offsets are computed once
+// per lane and advanced by a scalar per chunk, and every kernel argument is
+// loaded into SGPRs in one batch before the first copy (otherwise the
+// argument loads trail the copies, one cold scalar round trip each).
 //
 // Filter.  Each of the 4 waves owns 16*FN output channels and keeps its
 // whole filter slice (16*FN x r*s*c bytes, kSteps 64-byte k-steps) in VGPRs
@@ -37,6 +47,8 @@
 // the next pass computes while those stores drain.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "i8conv_internal.hpp"
 
 namespace i8conv {
@@ -50,18 +62,29 @@ __device__ __forceinline__ v4i add_wrap(v4i a, v4i b) {
 constexpr int kPassFrags = 4;
 
 struct HaloArgs {
-  int wp;            // padded row width: w + 2*pad_w
   int hp;            // padded rows per image: h + 2*pad_h
   int pitch;         // LDS bytes per input pixel: c + 16
   int units;         // 16-byte units per pixel in LDS: c / 16 + 1
-  int input_bytes;   // LDS bytes of the input rows (whole 4 KB copy rounds)
-  int copies;        // buffer->LDS instructions per wave for the input rows
+  int row_copies;    // 1 KB copies per padded input row
+  int row_bytes;     // LDS bytes between consecutive rows
+  int input_bytes;   // LDS bytes of the input rows (rows * row_bytes)
   int ranges;        // pixel ranges per channel slice
   int ring;          // filter staging slots in LDS (1..kHaloRing)
   int total_frags;   // ceil(M / 16)
   int tiles_n;
-  FastDiv div_ohw, div_ow, div_wp, div_hp, div_units;
+  FastDiv div_ohw, div_ow, div_hp, div_units, div_row_copies;
 };
+
+// Loads every 32-bit word of a kernel-argument struct into SGPRs here, in
+// one batch, instead of where each field is first used.
+template <class T>
+__device__ __forceinline__ void pin_sgprs(const T &v) {
+  static_assert(sizeof(T) % 4 == 0, "argument block of whole words");
+  uint32_t w[sizeof(T) / 4];
+  __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+  for (int i = 0; i < int(sizeof(T) / 4); ++i) asm volatile("" ::"s"(w[i]));
+}
 
 // Virtual padded row of output pixel m's tap-0 row; also returns its column.
 __device__ __forceinline__ int pixel_vrow(const ConvArgs &a, const HaloArgs &p, int m, int &ox) {
@@ -80,11 +103,11 @@ __device__ __forceinline__ int step_offset(const ConvArgs &a, const HaloArgs &p,
   const int c0 = k0 - tap * a.c;
   const int fy = int(fast_div(uint32_t(tap), a.div_s));
   const int fx = tap - fy * a.s;
-  return (fy * a.dil_h * p.wp + fx * a.dil_w) * p.pitch + c0;
+  return fy * a.dil_h * p.row_bytes + fx * a.dil_w * p.pitch + c0;
 }
 
 // The filter staging ring: chunk c = bytes [128c, 128c + 128) of the
-// workgroup's 64*FN filter rows.
+// workgroup's 64*FN filter rows, in ring slot c % slots.
 template <int FN, int kSteps>
 struct FilterRing {
   static constexpr int kRows = 64 * FN;
@@ -94,19 +117,31 @@ struct FilterRing {
   v4u wd;
   uint32_t lds;  // LDS address of slot 0
   const int8_t *ptr;
-  int slots, tile_n, wave, lane, gemm_k, gemm_n;
+  int slots, wave, lane;
+  mutable int cur;  // ring slot of the next chunk take() waits for
+  // Per copy j of this lane: the filter byte offset of its 16 bytes in
+  // chunk 0, and the bound on 128*c below which chunk c's bytes exist (0
+  // for channels past N, so every chunk reads zeros there).
+  uint32_t base[kCopies];
+  int klim[kCopies];
 
-  __device__ __forceinline__ void issue(int c) const {
+  __device__ __forceinline__ void init(int tile_n, int gemm_n, int gemm_k) {
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
-      const int inst = wave + 4 * j;
-      const int slot = inst * 64 + lane;
+      const int slot = (wave + 4 * j) * 64 + lane;
       const int r = slot >> 3;
       const int chunk16 = (slot & 7) ^ (r & 7) ^ ((r >> 3) & 1);  // inverse of swz128
       const int oc = tile_n + r;
-      const int k = c * 128 + chunk16 * 16;
-      const uint32_t off = oc < gemm_n && k < gemm_k ? uint32_t(oc * gemm_k + k) : kOutOfRange;
-      lds_copy16(wd, lds + (c % slots) * kChunkBytes + inst * 1024, off);
+      base[j] = uint32_t(oc) * uint32_t(gemm_k) + uint32_t(chunk16 * 16);
+      klim[j] = oc < gemm_n ? gemm_k - chunk16 * 16 : 0;
+    }
+  }
+  // Copies chunk c into ring slot `slot` (== c % slots).
+  __device__ __forceinline__ void issue(int c, int slot) const {
+#pragma unroll
+    for (int j = 0; j < kCopies; ++j) {
+      const uint32_t off = c * 128 < klim[j] ? base[j] + uint32_t(c * 128) : kOutOfRange;
+      lds_copy16(wd, lds + slot * kChunkBytes + (wave + 4 * j) * 1024, off);
     }
   }
   // Chunk c has landed once no more than `after` later chunks are
@@ -126,11 +161,14 @@ struct FilterRing {
     }
   }
   // Waits for chunk c, moves its two k-steps into this wave's fragments and
-  // refills its slot with chunk c + slots.
+  // refills its slot with chunk c + slots.  Chunks are taken in order, so
+  // `cur` (the slot of the next chunk to take) advances by one per take.
   __device__ __forceinline__ void take(int c, v4i (&wf)[kSteps][FN]) const {
     wait(c);
     __syncthreads();
-    const int8_t *src = ptr + (c % slots) * kChunkBytes;
+    const int slot = cur;
+    cur = slot + 1 == slots ? 0 : slot + 1;
+    const int8_t *src = ptr + slot * kChunkBytes;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int t = 2 * c + h;
@@ -142,7 +180,7 @@ struct FilterRing {
     }
     if (c + slots < kChunks) {
       __syncthreads();  // every wave has read this slot
-      issue(c + slots);
+      issue(c + slots, slot);
     }
   }
 };
@@ -153,7 +191,7 @@ struct FilterRing {
 template <int FN, int kSteps, int NF, bool kStage>
 __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
                                           const int8_t *smem, const FilterRing<FN, kSteps> &ring,
-                                          v4i (&wf)[kSteps][FN], const v4i (&bv)[FN],
+                                          v4i (&wf)[kSteps][FN], const int8_t *bias_lds,
                                           const int (&soff)[kSteps], int f0, int vr0, int m_first,
                                           int tile_n, int wave, int lane) {
   int vaddr[NF];
@@ -165,7 +203,7 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
     if (mpx[j] < 0) m = m_first;  // past the last pixel: computed, never stored
     int ox;
     const int vr = pixel_vrow(a, p, m, ox);
-    vaddr[j] = ((vr - vr0) * p.wp + ox * a.stride_w) * p.pitch + 16 * (lane >> 4);
+    vaddr[j] = (vr - vr0) * p.row_bytes + ox * a.stride_w * p.pitch + 16 * (lane >> 4);
   }
   v4i acc[NF][FN];
 #pragma unroll
@@ -173,12 +211,15 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
 #pragma unroll
     for (int i = 0; i < FN; ++i) acc[j][i] = v4i{0, 0, 0, 0};
 
+  // The staging pass takes chunk 0 before its first B reads: that wait and
+  // barrier are also what make every wave's input-row copies visible.
+  if (kStage) ring.take(0, wf);
   v4i bcur[NF], bnxt[NF];
 #pragma unroll
   for (int j = 0; j < NF; ++j) bcur[j] = *reinterpret_cast<const v4i *>(smem + vaddr[j] + soff[0]);
 #pragma unroll
   for (int t = 0; t < kSteps; ++t) {
-    if (kStage && (t & 1) == 0) ring.take(t >> 1, wf);
+    if (kStage && t > 0 && (t & 1) == 0) ring.take(t >> 1, wf);
     if (t + 1 < kSteps) {  // next step's B fragments, one step ahead of use
 #pragma unroll
       for (int j = 0; j < NF; ++j)
@@ -197,6 +238,11 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
     }
   }
 
+  // this wave's bias, staged in LDS by the first copy (see the prologue)
+  v4i bv[FN];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+    bv[i] = *reinterpret_cast<const v4i *>(bias_lds + (i * 16 + 4 * (lane >> 4)) * 4);
   const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
 #pragma unroll
   for (int j = 0; j < NF; ++j) {
@@ -218,12 +264,16 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
 }
 
 template <int FN, int kSteps>
-__global__ __launch_bounds__(kThreads, 1) void halo_kernel(ConvArgs a, HaloArgs p) {
+__global__ __launch_bounds__(kThreads, 1) void halo_kernel(ConvArgs a_arg, HaloArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  const ConvArgs a = a_arg;
+  const HaloArgs p = p_arg;
+  pin_sgprs(a);
+  pin_sgprs(p);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   const int tn = int(blockIdx.x) % p.tiles_n;
   const int range = int(blockIdx.x) / p.tiles_n;
@@ -231,53 +281,61 @@ __global__ __launch_bounds__(kThreads, 1) void halo_kernel(ConvArgs a, HaloArgs 
   const int f_end = int((int64_t(range + 1) * p.total_frags) / p.ranges);
   const int tile_n = tn * 64 * FN;
 
-  // bias of this lane's four channels per fragment (issued first: every
-  // later wait on the copies also covers these loads)
-  v4i bv[FN];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-    bv[i] = load_bias4(a.bias, a.gemm_n, tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4));
+  // ---- 0. bias of this wave's 16*FN channels -> LDS [wave * 256, +256) ----
+  // The first copy of every wave, so each later wait on the copy stream also
+  // covers it (its register form would need a compiler-inserted wait, which
+  // cannot see these copies and so waits for everything, stores included).
+  const int8_t *bias_lds = smem + wave * 256;
+  {
+    const int oc = tile_n + wave * 16 * FN + lane;
+    const uint32_t off = lane < 16 * FN && oc < a.gemm_n ? uint32_t(oc) * 4u : kOutOfRange;
+    lds_copy4(make_desc(a.bias, uint32_t(a.gemm_n) * 4u), lds_addr(bias_lds), off);
+  }
 
   const v4u xd = make_desc(a.x, a.x_bytes);
-  const uint32_t lds0 = lds_addr(smem);
+  const int8_t *rows = smem + kHaloBiasLds;
+  const uint32_t lds0 = lds_addr(rows);
   int ox_unused;
   const int m_first = f_begin * 16;
   const int m_last = min(f_end * 16, a.gemm_m) - 1;
-  const int vr0 = pixel_vrow(a, p, m_first, ox_unused);
-  const int vr1 = pixel_vrow(a, p, m_last, ox_unused) + (a.r - 1) * a.dil_h;
-  const int pixels = (vr1 - vr0 + 1) * p.wp;  // input pixels of the range
+  const int vr0 = __builtin_amdgcn_readfirstlane(pixel_vrow(a, p, m_first, ox_unused));
+  const int vr1 = __builtin_amdgcn_readfirstlane(pixel_vrow(a, p, m_last, ox_unused)) +
+                  (a.r - 1) * a.dil_h;
 
-  // ---- 1. input rows (whole pixels) -> LDS ----------------------------------
-  for (int j = 0; j < p.copies; ++j) {
-    const int inst = wave + 4 * j;
-    const int slot = inst * 64 + lane;  // 16-byte unit; `units` per pixel
+  // ---- 1. input rows -> LDS ------------------------------------------------
+  // Copy q covers units [64j, 64j + 64) of row rr (q = rr * row_copies + j).
+  // Unit `slot` of a row is unit u of padded column pix (slot = pix*units +
+  // u); unit units-1 is the pad.  Its byte offset in x is
+  //   ((b*h + iy)*w + pix - pad_w)*c + 16u = row_off + 16*(slot - pix).
+  const int copies = (vr1 - vr0 + 1) * p.row_copies;
+  for (int q = wave; q < copies; q += 4) {
+    const int rr = int(fast_div(uint32_t(q), p.div_row_copies));
+    const int j = q - rr * p.row_copies;
+    const int vr = vr0 + rr;
+    const int b = int(fast_div(uint32_t(vr), p.div_hp));
+    const int iy = vr - b * p.hp - a.pad_h;
+    const bool row_ok = b < a.n && unsigned(iy) < unsigned(a.h);
+    // modulo 2^32: exact wherever it is used (the sum below is in [0, 2^31))
+    const uint32_t row_off = uint32_t((b * a.h + iy) * a.wd - a.pad_w) * uint32_t(a.c);
+    const int slot = j * 64 + lane;
     const int pix = int(fast_div(uint32_t(slot), p.div_units));
-    const int u = slot - pix * p.units;
-    uint32_t off = kOutOfRange;
-    if (u < p.units - 1 && pix < pixels) {
-      const int rr = int(fast_div(uint32_t(pix), p.div_wp));
-      const int px = pix - rr * p.wp - a.pad_w;
-      const int vr = vr0 + rr;
-      const int b = int(fast_div(uint32_t(vr), p.div_hp));
-      const int iy = vr - b * p.hp - a.pad_h;
-      if (b < a.n && unsigned(iy) < unsigned(a.h) && unsigned(px) < unsigned(a.wd))
-        off = uint32_t(((b * a.h + iy) * a.wd + px) * a.c + u * 16);
-    }
-    lds_copy16(xd, lds0 + inst * 1024, off);
+    const bool ok = row_ok && slot - pix * p.units < p.units - 1 &&
+                    unsigned(pix - a.pad_w) < unsigned(a.wd);
+    const uint32_t off = ok ? row_off + uint32_t(16 * (slot - pix)) : kOutOfRange;
+    lds_copy16(xd, lds0 + rr * p.row_bytes + j * 1024, off);
   }
 
   // ---- 2. start the filter ring --------------------------------------------
   FilterRing<FN, kSteps> ring;
   ring.wd = make_desc(a.w, a.w_bytes);
-  ring.ptr = smem + p.input_bytes;
+  ring.ptr = rows + p.input_bytes;
   ring.lds = lds_addr(ring.ptr);
   ring.slots = p.ring;
-  ring.tile_n = tile_n;
+  ring.cur = 0;
   ring.wave = wave;
   ring.lane = lane;
-  ring.gemm_k = a.gemm_k;
-  ring.gemm_n = a.gemm_n;
-  for (int c = 0; c < ring.slots && c < ring.kChunks; ++c) ring.issue(c);
+  ring.init(tile_n, a.gemm_n, a.gemm_k);
+  for (int c = 0; c < ring.slots && c < ring.kChunks; ++c) ring.issue(c, c);
 
   // ---- 3. passes of up to four fragments -------------------------------------
   int soff[kSteps];
@@ -288,19 +346,19 @@ __global__ __launch_bounds__(kThreads, 1) void halo_kernel(ConvArgs a, HaloArgs 
   {
     const int nf = min(kPassFrags, f_end - f0);
     switch (nf) {
-      case 4: halo_pass<FN, kSteps, 4, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
-      case 3: halo_pass<FN, kSteps, 3, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
-      case 2: halo_pass<FN, kSteps, 2, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
-      default: halo_pass<FN, kSteps, 1, true>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 4: halo_pass<FN, kSteps, 4, true>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 3: halo_pass<FN, kSteps, 3, true>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 2: halo_pass<FN, kSteps, 2, true>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      default: halo_pass<FN, kSteps, 1, true>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
     }
     f0 += nf;
   }
   for (; f0 < f_end; f0 += kPassFrags) {
     switch (min(kPassFrags, f_end - f0)) {
-      case 4: halo_pass<FN, kSteps, 4, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
-      case 3: halo_pass<FN, kSteps, 3, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
-      case 2: halo_pass<FN, kSteps, 2, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
-      default: halo_pass<FN, kSteps, 1, false>(a, p, smem, ring, wf, bv, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 4: halo_pass<FN, kSteps, 4, false>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 3: halo_pass<FN, kSteps, 3, false>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      case 2: halo_pass<FN, kSteps, 2, false>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
+      default: halo_pass<FN, kSteps, 1, false>(a, p, rows, ring, wf, bias_lds, soff, f0, vr0, m_first, tile_n, wave, lane); break;
     }
   }
 }
@@ -333,36 +391,32 @@ bool halo_instance_exists(int fn, int steps) {
          (fn == 2 && (steps == 9 || steps == 18));
 }
 
-size_t halo_input_copies(int pixels, int channels) {
-  // (c/16 + 1) 16-byte units per pixel; 4 waves x 64 units per round
-  return (size_t(pixels) * size_t(channels / 16 + 1) + 255) / 256;
-}
-
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream) {
+  const HaloRowLayout row = halo_row_layout(a.wd + 2 * a.pad_w, a.c);
+  const int fn = p.bn / 64;
+  const size_t lds = size_t(kHaloBiasLds) + size_t(p.rows) * size_t(row.row_bytes) +
+                     size_t(p.ring) * halo_ring_slot_bytes(fn);
   HaloArgs h{};
-  h.wp = a.wd + 2 * a.pad_w;
   h.hp = a.h + 2 * a.pad_h;
   h.pitch = a.c + 16;
-  h.units = a.c / 16 + 1;
-  h.copies = p.copies;
-  h.input_bytes = p.copies * 4 * 1024;
+  h.units = int(row.units);
+  h.row_copies = int(row.row_copies);
+  h.row_bytes = int(std::min<int64_t>(row.row_bytes, kLdsBudget));
+  h.input_bytes = int(std::min<size_t>(size_t(p.rows) * size_t(h.row_bytes), kLdsBudget));
   h.ranges = p.ranges;
   h.ring = p.ring;
   h.total_frags = (a.gemm_m + 15) / 16;
   h.tiles_n = p.tiles_n;
   h.div_ohw = make_fastdiv(uint32_t(a.out_h * a.out_w));
   h.div_ow = make_fastdiv(uint32_t(a.out_w));
-  h.div_wp = make_fastdiv(uint32_t(h.wp));
   h.div_hp = make_fastdiv(uint32_t(h.hp));
   h.div_units = make_fastdiv(uint32_t(h.units));
-  const int fn = p.bn / 64;
-  const size_t lds = size_t(h.input_bytes) + size_t(p.ring) * halo_ring_slot_bytes(fn);
+  h.div_row_copies = make_fastdiv(uint32_t(h.row_copies));
   const size_t blocks = size_t(p.ranges) * p.tiles_n;
   const int steps = a.gemm_k / 64;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a.c % 64 != 0 || !halo_instance_exists(fn, steps) || lds > size_t(kLdsBudget) ||
-      a.c / 16 + 1 > 255 ||
-      p.ring < 1 || p.ring > kHaloRing) {
+      p.rows < 1 || p.ranges < 1 || p.ring < 1 || p.ring > kHaloRing) {
     set_error("halo plan out of range");
     return I8CONV_BAD_ARGUMENT;
   }

@@ -146,6 +146,8 @@ bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p
     const int64_t oy = (m % (int64_t(g.out_h) * g.out_w)) / g.out_w;
     return b * hp + oy * s.stride_h;
   };
+  const HaloRowLayout row = halo_row_layout(wp, s.c);
+  if (row.row_bytes > kLdsBudget) return false;
   const int64_t first = std::max<int64_t>(1, std::min(total_frags, ceil_div(256, tiles_n)));
   const int64_t chunks = ceil_div(g.gemm_k, 128);
   for (int64_t ranges = first; ranges <= total_frags;
@@ -153,18 +155,18 @@ bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p
     // each workgroup re-reads the whole filter slice: beyond the first grid
     // that fills the compute units, keep at least four fragments per range
     if (ranges > first && total_frags / ranges < 4) break;
-    int64_t max_slots = 0;
+    int64_t max_rows = 0;
     for (int64_t r = 0; r < ranges; ++r) {
       const int64_t f0 = r * total_frags / ranges, f1 = (r + 1) * total_frags / ranges;
       if (f1 <= f0) continue;
       const int64_t m0 = f0 * 16, m1 = std::min<int64_t>(f1 * 16, g.gemm_m) - 1;
       const int64_t rows = vrow(m1) - vrow(m0) + int64_t(s.r - 1) * s.dilation_h + 1;
-      max_slots = std::max(max_slots, rows * wp);
+      max_rows = std::max(max_rows, rows);
     }
-    const int64_t copies = int64_t(halo_input_copies(int(std::min<int64_t>(max_slots, INT32_MAX)), s.c));
-    const int64_t input_lds = copies * 4096;
+    const int64_t input_lds = kHaloBiasLds + max_rows * row.row_bytes;
     const int64_t slot = int64_t(halo_ring_slot_bytes(fn));
-    const int64_t ring = std::min<int64_t>({kHaloRing, chunks, (kLdsBudget - input_lds) / slot});
+    const int64_t ring = input_lds >= kLdsBudget ? 0 :
+        std::min<int64_t>({kHaloRing, chunks, (kLdsBudget - input_lds) / slot});
     if (ring >= 1 && ranges * tiles_n <= INT32_MAX) {
       p->ring = int(ring);
       p->resident = true;
@@ -172,11 +174,11 @@ bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p
       p->bn = 64 * fn;
       p->tiles_n = tiles_n;
       p->ranges = int(ranges);
-      p->copies = int(copies);
+      p->rows = int(max_rows);
       p->frags_m = int(ceil_div(total_frags, ranges));
       p->th = p->tw = p->ph = p->pw = 0;
       p->tiles_y = p->tiles_x = 1;
-      p->stage_pixels = int(max_slots);
+      p->stage_pixels = int(max_rows * wp);
       return true;
     }
     if (ranges == total_frags) break;
