@@ -48,7 +48,21 @@ inline FastDiv make_fastdiv(uint32_t d) {
   return f;
 }
 
-I8_HD inline uint32_t fast_div(uint32_t n, const FastDiv &f) {
+// The same divider without the divisor: three words, for kernels that keep
+// every argument in SGPRs.
+struct FastDiv3 {
+  uint32_t mul;
+  uint32_t add;
+  uint32_t shift;
+};
+
+inline FastDiv3 make_fastdiv3(uint32_t d) {
+  const FastDiv f = make_fastdiv(d);
+  return FastDiv3{f.mul, f.add, f.shift};
+}
+
+template <class D>
+I8_HD inline uint32_t fast_div(uint32_t n, const D &f) {
   const uint32_t hi = uint32_t((uint64_t(n) * f.mul) >> 32);
   return (hi + (f.add ? n : 0u)) >> f.shift;
 }

@@ -38,8 +38,9 @@
 // 16 rows x 64 bytes (16 half-used cache lines) and streams at a third of
 // the rate of whole-line reads, so the slice is fetched with whole-line
 // copies (8 rows x 128 bytes per instruction) into an LDS ring of up to 8
-// slots (swz128 layout) and picked out of LDS in fragment order.  The first
-// pass consumes each 128-byte chunk as soon as it lands, so the filter fetch
+// slots (swz128 layout) and picked out of LDS in fragment order.  Each wave
+// copies its own rows, so the ring needs no barriers.  The first pass
+// consumes each 128-byte chunk as soon as it lands, so the filter fetch
 // overlaps that pass's MFMAs.
 //
 // Compute.  Fragments run up to four at a time through all k-steps (B
@@ -107,7 +108,10 @@ __device__ __forceinline__ int step_offset(const ConvArgs &a, const HaloArgs &p,
 }
 
 // The filter staging ring: chunk c = bytes [128c, 128c + 128) of the
-// workgroup's 64*FN filter rows, in ring slot c % slots.
+// workgroup's 64*FN filter rows, in ring slot c % slots.  Each wave copies
+// and reads only its own 16*FN rows of every slot, so a chunk needs no
+// barrier: the wave's own copy counter says when its rows have landed, and
+// only the wave itself reuses them.
 template <int FN, int kSteps>
 struct FilterRing {
   static constexpr int kRows = 64 * FN;
@@ -128,7 +132,7 @@ struct FilterRing {
   __device__ __forceinline__ void init(int tile_n, int gemm_n, int gemm_k) {
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
-      const int slot = (wave + 4 * j) * 64 + lane;
+      const int slot = (kCopies * wave + j) * 64 + lane;  // rows 16*FN*wave + [0, 16*FN)
       const int r = slot >> 3;
       const int chunk16 = (slot & 7) ^ (r & 7) ^ ((r >> 3) & 1);  // inverse of swz128
       const int oc = tile_n + r;
@@ -141,7 +145,7 @@ struct FilterRing {
 #pragma unroll
     for (int j = 0; j < kCopies; ++j) {
       const uint32_t off = c * 128 < klim[j] ? base[j] + uint32_t(c * 128) : kOutOfRange;
-      lds_copy16(wd, lds + slot * kChunkBytes + (wave + 4 * j) * 1024, off);
+      lds_copy16(wd, lds + slot * kChunkBytes + (kCopies * wave + j) * 1024, off);
     }
   }
   // Chunk c has landed once no more than `after` later chunks are
@@ -163,9 +167,12 @@ struct FilterRing {
   // Waits for chunk c, moves its two k-steps into this wave's fragments and
   // refills its slot with chunk c + slots.  Chunks are taken in order, so
   // `cur` (the slot of the next chunk to take) advances by one per take.
+  // Taking chunk 0 also publishes the input rows: every wave has then waited
+  // for its own row copies (older than its chunk-0 copies), and one barrier
+  // makes all of them visible to all waves.
   __device__ __forceinline__ void take(int c, v4i (&wf)[kSteps][FN]) const {
     wait(c);
-    __syncthreads();
+    if (c == 0) __syncthreads();
     const int slot = cur;
     cur = slot + 1 == slots ? 0 : slot + 1;
     const int8_t *src = ptr + slot * kChunkBytes;
@@ -179,7 +186,8 @@ struct FilterRing {
             src + swz128(wave * 16 * FN + i * 16 + (lane & 15), 4 * h + (lane >> 4)));
     }
     if (c + slots < kChunks) {
-      __syncthreads();  // every wave has read this slot
+      // this wave's reads of its rows must be done before they are refilled
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       issue(c + slots, slot);
     }
   }
