@@ -261,11 +261,11 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
       const v4i v = add_wrap(acc[j][i], bv[i]);
       int32_t *dst = a.y + size_t(mpx[j]) * size_t(a.gemm_n) + oc0;
       if (vec) {
-        if (oc0 < a.gemm_n) *reinterpret_cast<v4i *>(dst) = v;
+        if (oc0 < a.gemm_n) store_out4(dst, v);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (oc0 + e < a.gemm_n) dst[e] = v[e];
+          if (oc0 + e < a.gemm_n) store_out1(dst + e, v[e]);
       }
     }
   }
