@@ -95,7 +95,16 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
     PatchPlan p;
     if (id == I8CONV_KERNEL_STRIP) plan_strip(*shape, g, &p);
     else plan_halo(*shape, g, &p);
-    if (p.resident) {
+    if (p.row) {
+      const size_t row_bytes =
+          size_t(halo_row_layout(shape->w + 2 * shape->pad_w, shape->c).row_bytes);
+      d = std::string(kNames[id]) + " row-streaming: " + std::to_string(p.ranges) +
+          " row blocks/image of <=" + std::to_string(p.rows - 2) + " rows x " +
+          std::to_string(p.bn) + "oc, " + std::to_string(p.frags_m) + " frags/row, LDS " +
+          std::to_string((kHaloBiasLds + size_t(p.rows) * row_bytes) / 1024) + "+" +
+          std::to_string(p.ring * halo_ring_slot_bytes(p.bn / 64) / 1024) + " KB, grid " +
+          std::to_string(int64_t(shape->n) * p.ranges * p.tiles_n);
+    } else if (p.resident) {
       d = std::string(kNames[id]) + " resident rows: " + std::to_string(p.ranges) +
           " pixel ranges of <=" + std::to_string(p.frags_m * 16) + "px x " +
           std::to_string(p.bn) + "oc, LDS " +
@@ -163,8 +172,9 @@ int i8conv_launch(int id, const i8conv_shape *shape, const int8_t *input,
         set_error(std::string(kNames[id]) + " is not eligible for this shape");
         return I8CONV_INELIGIBLE;
       }
-      return pp.resident ? launch_halo_resident(args, pp, stream)
-                         : launch_patch(args, pp, stream);
+      return pp.row ? launch_row(args, pp, stream)
+             : pp.resident ? launch_halo_resident(args, pp, stream)
+                           : launch_patch(args, pp, stream);
     }
     case I8CONV_KERNEL_SPLITK: {
       if (!i8conv_eligible(id, shape)) {
@@ -322,7 +332,7 @@ int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
   hipEvent_t start, stop;
   if ((e = hipEventCreate(&start)) != hipSuccess) return hip_fail("hipEventCreate", e);
   if ((e = hipEventCreate(&stop)) != hipSuccess) {
-    hipEventDestroy(start);
+    (void)hipEventDestroy(start);
     return hip_fail("hipEventCreate", e);
   }
   int rc = I8CONV_OK;
@@ -350,8 +360,9 @@ int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
     if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) rc = hip_fail("hipEventElapsedTime", e);
     if (rc == I8CONV_OK) *batched_ms = ms / float(iterations);
   }
-  hipEventDestroy(start);
-  hipEventDestroy(stop);
+  // teardown: a failure here cannot change the measured result
+  (void)hipEventDestroy(start);
+  (void)hipEventDestroy(stop);
   return rc;
 }
 

@@ -51,6 +51,9 @@ struct PatchPlan {
   // halo only: flattened pixel ranges with their input rows of every channel
   // group resident in LDS and the filter slice in registers (kernel_halo.hip)
   bool resident = false;
+  // halo, 3x3 stride 1: output-row blocks streamed row by row with the
+  // taps formed in registers (kernel_row.hip); `ranges` = blocks per image
+  bool row = false;
   int ranges = 0;  // resident: pixel ranges per channel slice
   int rows = 0;    // resident: most padded input rows any range needs
   int ring = 0;    // resident: filter staging slots in LDS
@@ -71,6 +74,10 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
                   void *stream);
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
+int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream);
+// Whether kernel_row.hip has an instance for 16*fn channels per wave, cg
+// 64-channel groups and nfr 16-column fragments per output row.
+bool row_instance_exists(int fn, int cg, int nfr);
 // Whether kernel_halo.hip has an instance for 16*fn channels per wave and
 // `steps` 64-byte k-steps.
 bool halo_instance_exists(int fn, int steps);

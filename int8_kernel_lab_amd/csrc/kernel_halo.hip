@@ -50,15 +50,11 @@
 
 #include <algorithm>
 
-#include "i8conv_internal.hpp"
+#include "halo_common.hpp"
 
 namespace i8conv {
 namespace {
 
-__device__ __forceinline__ v4i add_wrap(v4i a, v4i b) {
-  return __builtin_bit_cast(v4i, __builtin_bit_cast(v4u, a) +
-                                     __builtin_bit_cast(v4u, b));
-}
 
 constexpr int kPassFrags = 4;
 
@@ -75,17 +71,6 @@ struct HaloArgs {
   int tiles_n;
   FastDiv div_ohw, div_ow, div_hp, div_units, div_row_copies;
 };
-
-// Loads every 32-bit word of a kernel-argument struct into SGPRs here, in
-// one batch, instead of where each field is first used.
-template <class T>
-__device__ __forceinline__ void pin_sgprs(const T &v) {
-  static_assert(sizeof(T) % 4 == 0, "argument block of whole words");
-  uint32_t w[sizeof(T) / 4];
-  __builtin_memcpy(w, &v, sizeof(T));
-#pragma unroll
-  for (int i = 0; i < int(sizeof(T) / 4); ++i) asm volatile("" ::"s"(w[i]));
-}
 
 // Virtual padded row of output pixel m's tap-0 row; also returns its column.
 __device__ __forceinline__ int pixel_vrow(const ConvArgs &a, const HaloArgs &p, int m, int &ox) {
@@ -106,92 +91,6 @@ __device__ __forceinline__ int step_offset(const ConvArgs &a, const HaloArgs &p,
   const int fx = tap - fy * a.s;
   return fy * a.dil_h * p.row_bytes + fx * a.dil_w * p.pitch + c0;
 }
-
-// The filter staging ring: chunk c = bytes [128c, 128c + 128) of the
-// workgroup's 64*FN filter rows, in ring slot c % slots.  Each wave copies
-// and reads only its own 16*FN rows of every slot, so a chunk needs no
-// barrier: the wave's own copy counter says when its rows have landed, and
-// only the wave itself reuses them.
-template <int FN, int kSteps>
-struct FilterRing {
-  static constexpr int kRows = 64 * FN;
-  static constexpr int kChunks = (kSteps + 1) / 2;
-  static constexpr int kChunkBytes = kRows * 128;
-  static constexpr int kCopies = kRows * 8 / 64 / 4;  // per wave per chunk
-  v4u wd;
-  uint32_t lds;  // LDS address of slot 0
-  const int8_t *ptr;
-  int slots, wave, lane;
-  mutable int cur;  // ring slot of the next chunk take() waits for
-  // Per copy j of this lane: the filter byte offset of its 16 bytes in
-  // chunk 0, and the bound on 128*c below which chunk c's bytes exist (0
-  // for channels past N, so every chunk reads zeros there).
-  uint32_t base[kCopies];
-  int klim[kCopies];
-
-  __device__ __forceinline__ void init(int tile_n, int gemm_n, int gemm_k) {
-#pragma unroll
-    for (int j = 0; j < kCopies; ++j) {
-      const int slot = (kCopies * wave + j) * 64 + lane;  // rows 16*FN*wave + [0, 16*FN)
-      const int r = slot >> 3;
-      const int chunk16 = (slot & 7) ^ (r & 7) ^ ((r >> 3) & 1);  // inverse of swz128
-      const int oc = tile_n + r;
-      base[j] = uint32_t(oc) * uint32_t(gemm_k) + uint32_t(chunk16 * 16);
-      klim[j] = oc < gemm_n ? gemm_k - chunk16 * 16 : 0;
-    }
-  }
-  // Copies chunk c into ring slot `slot` (== c % slots).
-  __device__ __forceinline__ void issue(int c, int slot) const {
-#pragma unroll
-    for (int j = 0; j < kCopies; ++j) {
-      const uint32_t off = c * 128 < klim[j] ? base[j] + uint32_t(c * 128) : kOutOfRange;
-      lds_copy16(wd, lds + slot * kChunkBytes + (kCopies * wave + j) * 1024, off);
-    }
-  }
-  // Chunk c has landed once no more than `after` later chunks are
-  // outstanding: copies return in issue order, and everything issued before
-  // the ring (bias, input rows) is older than every chunk.
-  __device__ __forceinline__ void wait(int c) const {
-    const int after = min(slots - 1, kChunks - 1 - c);
-    switch (after) {
-      case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-      case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(1 * kCopies) : "memory"); break;
-      case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kCopies) : "memory"); break;
-      case 3: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * kCopies) : "memory"); break;
-      case 4: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * kCopies) : "memory"); break;
-      case 5: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * kCopies) : "memory"); break;
-      case 6: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * kCopies) : "memory"); break;
-      default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(7 * kCopies) : "memory"); break;
-    }
-  }
-  // Waits for chunk c, moves its two k-steps into this wave's fragments and
-  // refills its slot with chunk c + slots.  Chunks are taken in order, so
-  // `cur` (the slot of the next chunk to take) advances by one per take.
-  // Taking chunk 0 also publishes the input rows: every wave has then waited
-  // for its own row copies (older than its chunk-0 copies), and one barrier
-  // makes all of them visible to all waves.
-  __device__ __forceinline__ void take(int c, v4i (&wf)[kSteps][FN]) const {
-    wait(c);
-    if (c == 0) __syncthreads();
-    const int slot = cur;
-    cur = slot + 1 == slots ? 0 : slot + 1;
-    const int8_t *src = ptr + slot * kChunkBytes;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int t = 2 * c + h;
-      if (t >= kSteps) break;
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-        wf[t][i] = *reinterpret_cast<const v4i *>(
-            src + swz128(wave * 16 * FN + i * 16 + (lane & 15), 4 * h + (lane >> 4)));
-    }
-    if (c + slots < kChunks) {
-      // this wave's reads of its rows must be done before they are refilled
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      issue(c + slots, slot);
-    }
-  }
-};
 
 // NF fragments starting at f0 through all k-steps, then bias + stores.  The
 // staging pass (kStage) also pulls the filter out of the ring, chunk by chunk,
@@ -258,7 +157,7 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
       const int oc0 = tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4);
-      const v4i v = add_wrap(acc[j][i], bv[i]);
+      const v4i v = add_wrap4(acc[j][i], bv[i]);
       int32_t *dst = a.y + size_t(mpx[j]) * size_t(a.gemm_n) + oc0;
       if (vec) {
         if (oc0 < a.gemm_n) store_out4(dst, v);
@@ -294,11 +193,7 @@ __global__ __launch_bounds__(kThreads, 1) void halo_kernel(ConvArgs a_arg, HaloA
   // covers it (its register form would need a compiler-inserted wait, which
   // cannot see these copies and so waits for everything, stores included).
   const int8_t *bias_lds = smem + wave * 256;
-  {
-    const int oc = tile_n + wave * 16 * FN + lane;
-    const uint32_t off = lane < 16 * FN && oc < a.gemm_n ? uint32_t(oc) * 4u : kOutOfRange;
-    lds_copy4(make_desc(a.bias, uint32_t(a.gemm_n) * 4u), lds_addr(bias_lds), off);
-  }
+  stage_bias<FN>(a.bias, a.gemm_n, tile_n + wave * 16 * FN, bias_lds, lane);
 
   const v4u xd = make_desc(a.x, a.x_bytes);
   const int8_t *rows = smem + kHaloBiasLds;
@@ -311,27 +206,9 @@ __global__ __launch_bounds__(kThreads, 1) void halo_kernel(ConvArgs a_arg, HaloA
                   (a.r - 1) * a.dil_h;
 
   // ---- 1. input rows -> LDS ------------------------------------------------
-  // Copy q covers units [64j, 64j + 64) of row rr (q = rr * row_copies + j).
-  // Unit `slot` of a row is unit u of padded column pix (slot = pix*units +
-  // u); unit units-1 is the pad.  Its byte offset in x is
-  //   ((b*h + iy)*w + pix - pad_w)*c + 16u = row_off + 16*(slot - pix).
-  const int copies = (vr1 - vr0 + 1) * p.row_copies;
-  for (int q = wave; q < copies; q += 4) {
-    const int rr = int(fast_div(uint32_t(q), p.div_row_copies));
-    const int j = q - rr * p.row_copies;
-    const int vr = vr0 + rr;
-    const int b = int(fast_div(uint32_t(vr), p.div_hp));
-    const int iy = vr - b * p.hp - a.pad_h;
-    const bool row_ok = b < a.n && unsigned(iy) < unsigned(a.h);
-    // modulo 2^32: exact wherever it is used (the sum below is in [0, 2^31))
-    const uint32_t row_off = uint32_t((b * a.h + iy) * a.wd - a.pad_w) * uint32_t(a.c);
-    const int slot = j * 64 + lane;
-    const int pix = int(fast_div(uint32_t(slot), p.div_units));
-    const bool ok = row_ok && slot - pix * p.units < p.units - 1 &&
-                    unsigned(pix - a.pad_w) < unsigned(a.wd);
-    const uint32_t off = ok ? row_off + uint32_t(16 * (slot - pix)) : kOutOfRange;
-    lds_copy16(xd, lds0 + rr * p.row_bytes + j * 1024, off);
-  }
+  copy_input_rows(xd, lds0, vr0, vr1 - vr0 + 1, wave, lane, p.row_copies, p.div_row_copies,
+                  p.row_bytes, p.div_hp, p.hp, p.units, p.div_units, a.n, a.h, a.wd, a.c,
+                  a.pad_h, a.pad_w);
 
   // ---- 2. start the filter ring --------------------------------------------
   FilterRing<FN, kSteps> ring;

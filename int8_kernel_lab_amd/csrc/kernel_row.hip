@@ -1,0 +1,374 @@
+// Row-streaming 3x3 kernel on gfx950 INT8 MFMA: the halo-tiled variant for
+// stride-1, dilation-1 3x3 layers, built so that each input byte staged in
+// LDS is read once per channel group instead of once per tap.
+//
+// Work split.  A workgroup takes a block of consecutive output rows of one
+// image (and one 64*FN-channel slice of K); its padded input rows (the block
+// plus two) are copied into LDS once, as in kernel_halo.hip.  Output rows are
+// cut into ceil(out_w / 16) fragments of 16 consecutive columns (NFR per row;
+// lanes past out_w are computed and dropped).
+//
+// Reuse.  The B fragment of tap (fy, fx) for output pixels (oy, x0..x0+15)
+// is input row oy + fy, columns x0 + fx .. x0 + fx + 15, and it is the same
+// fragment for the three output rows oy = ir - fy that input row ir feeds.
+// So the kernel walks the input rows once: for input row ir and channel
+// group cg it reads the 3 * NFR fragments at column offsets fx = 0, 1, 2 (one
+// LDS read each) and feeds each one to the output rows ir, ir - 1, ir - 2
+// (taps fy = 0, 1, 2), FN MFMAs per row, whose accumulators rotate through
+// three register sets: when input row ir is done, output row ir - 2 is
+// complete and is stored at once, so stores are spread over the whole
+// kernel.  Each B read feeds 3 * FN MFMAs (FN in a per-tap walk): about
+// 1024 / (3 * FN) LDS bytes per 16-cycle MFMA per SIMD, a third of the LDS
+// read rate, so the MFMAs are no longer fed at LDS speed.  (Forming the
+// fx = 1, 2 fragments from the fx = 0 ones with DPP lane moves would save
+// LDS reads the kernel does not need to save; the VALU moves contend with
+// the MFMA issue of the single wave per SIMD and measured slower.)
+//
+// Filter.  Each wave keeps its 16*FN channels x 9*c bytes in VGPRs for the
+// whole workgroup (stationary A).  It streams in through the same per-wave
+// LDS ring as in kernel_halo.hip, in k order (fy-major), and the first three
+// input rows only need taps fy <= ir, so the fetch overlaps their MFMAs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "halo_common.hpp"
+
+namespace i8conv {
+namespace {
+
+// Everything the kernel reads; loaded into SGPRs in one batch.
+struct RowArgs {
+  const int8_t *x;
+  const int8_t *w;
+  const int32_t *bias;
+  int32_t *y;
+  uint32_t x_bytes, w_bytes;
+  int n, h, wd, c, pad_h, pad_w;
+  int out_h, out_w, gemm_n, gemm_k;
+  int hp;           // padded rows per image: h + 2*pad_h
+  int wp;           // padded columns: w + 2*pad_w (== out_w + 2)
+  int pitch;        // LDS bytes per input pixel: c + 16
+  int units;        // 16-byte units per pixel in LDS: c / 16 + 1
+  int row_copies;   // 1 KB copies per padded input row
+  int row_bytes;    // LDS bytes between consecutive rows
+  int input_bytes;  // LDS bytes of the input rows
+  int blocks;       // output-row blocks per image
+  int ring;         // filter staging slots in LDS
+  int tiles_n;
+  FastDiv div_hp, div_units, div_row_copies, div_blocks, div_tiles_n;
+};
+
+template <int FN, int CG, int NFR>
+struct RowState {
+  static constexpr int kSteps = 9 * CG;
+  v4i wf[kSteps][FN];       // stationary filter fragments, k-step t = (fy*3 + fx)*CG + cg
+  v4i acc[3][NFR][FN];      // output rows ir, ir - 1, ir - 2 rotate through these
+  int colofs[3][NFR];       // LDS offset of this lane's column + fx / k-block in a row
+};
+
+// Input row ir (K == ir % 3, compile time, fixes the accumulator roles):
+// the fragments of every channel group at the three column offsets fx, and
+// the filter rows fy in MASK (bit fy; compile time, so the MFMAs of a row
+// form one straight-line block).  Each fragment feeds the output rows
+// ir - fy of every fy in MASK, FN MFMAs each.  With kCheck, a filter row
+// also needs 0 <= ir - fy < rows_out at run time (blocks of fewer than two
+// rows, whose first and last rows overlap).
+//
+// `frag` holds the fragments of (ir, channel group 0) on entry and those of
+// (ir + 1, channel group 0) on return: each group's reads are issued before
+// the MFMAs of the previous one, so with one wave per SIMD the LDS latency
+// is hidden behind MFMAs instead of stalling them.  The last input row (only
+// filter row 2 left: MASK 4, or 7 in a one-row block) reads row 0 again.
+template <int FN, int CG, int NFR, int K, int MASK, bool kCheck>
+__device__ __forceinline__ void row_step(const RowArgs &p, RowState<FN, CG, NFR> &st,
+                                         v4i (&frag)[3][NFR], const int8_t *rows,
+                                         const int8_t *bias_lds, int ir, int rows_out,
+                                         int m_row0, int tile_n, int wave, int lane) {
+  constexpr int s0 = K, s1 = (K + 2) % 3, s2 = (K + 1) % 3;  // sets of rows ir, ir-1, ir-2
+  if (MASK & 1) {  // output row ir starts here
+#pragma unroll
+    for (int j = 0; j < NFR; ++j)
+#pragma unroll
+      for (int i = 0; i < FN; ++i) st.acc[s0][j][i] = v4i{0, 0, 0, 0};
+  }
+  const bool v0 = (MASK & 1) && (!kCheck || ir < rows_out);
+  const bool v1 = (MASK & 2) && (!kCheck || (ir >= 1 && ir - 1 < rows_out));
+  const bool v2 = (MASK & 4) && (!kCheck || (ir >= 2 && ir - 2 < rows_out));
+  const int8_t *row = rows + ir * p.row_bytes;
+#pragma unroll
+  for (int cg = 0; cg < CG; ++cg) {
+    v4i cur[3][NFR];
+#pragma unroll
+    for (int fx = 0; fx < 3; ++fx)
+#pragma unroll
+      for (int j = 0; j < NFR; ++j) cur[fx][j] = frag[fx][j];
+    constexpr bool kLast = MASK == 4 || (kCheck && MASK == 7);
+    const int8_t *next = cg + 1 < CG ? row + (cg + 1) * 64 : kLast ? rows : row + p.row_bytes;
+#pragma unroll
+    for (int fx = 0; fx < 3; ++fx)
+#pragma unroll
+      for (int j = 0; j < NFR; ++j)
+        frag[fx][j] = *reinterpret_cast<const v4i *>(next + st.colofs[fx][j]);
+    // keep the reads here: the scheduler would otherwise sink them to their use
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int fx = 0; fx < 3; ++fx) {
+      if ((MASK & 1) && (!kCheck || v0)) {
+#pragma unroll
+        for (int j = 0; j < NFR; ++j)
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+            st.acc[s0][j][i] = mfma16(st.wf[(0 + fx) * CG + cg][i], cur[fx][j], st.acc[s0][j][i]);
+      }
+      if ((MASK & 2) && (!kCheck || v1)) {
+#pragma unroll
+        for (int j = 0; j < NFR; ++j)
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+            st.acc[s1][j][i] = mfma16(st.wf[(3 + fx) * CG + cg][i], cur[fx][j], st.acc[s1][j][i]);
+      }
+      if ((MASK & 4) && (!kCheck || v2)) {
+#pragma unroll
+        for (int j = 0; j < NFR; ++j)
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+            st.acc[s2][j][i] = mfma16(st.wf[(6 + fx) * CG + cg][i], cur[fx][j], st.acc[s2][j][i]);
+      }
+    }
+  }
+  if (!(MASK & 4) || (kCheck && !v2)) return;
+  // output row ir - 2 is complete: bias + stores
+  v4i bv[FN];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+    bv[i] = *reinterpret_cast<const v4i *>(bias_lds + (i * 16 + 4 * (lane >> 4)) * 4);
+  const bool vec = (p.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
+  const int m_row = m_row0 + (ir - 2) * p.out_w;
+#pragma unroll
+  for (int j = 0; j < NFR; ++j) {
+    const int col = 16 * j + (lane & 15);
+    if (col >= p.out_w) continue;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int oc0 = tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4);
+      const v4i v = add_wrap4(st.acc[s2][j][i], bv[i]);
+      int32_t *dst = p.y + size_t(m_row + col) * size_t(p.gemm_n) + oc0;
+      if (vec) {
+        if (oc0 < p.gemm_n) store_out4(dst, v);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (oc0 + e < p.gemm_n) store_out1(dst + e, v[e]);
+      }
+    }
+  }
+}
+
+// Takes ring chunks [C0, C1) (chunk c = k-steps 2c, 2c + 1) into st.wf.
+template <int FN, int CG, int NFR, int C0, int C1>
+__device__ __forceinline__ void take_chunks(FilterRing<FN, 9 * CG> &ring,
+                                            RowState<FN, CG, NFR> &st) {
+#pragma unroll
+  for (int c = C0; c < C1; ++c) ring.take(c, st.wf);
+}
+
+template <int FN, int CG, int NFR>
+__global__ __launch_bounds__(kThreads, 1) void row_kernel(RowArgs p_arg) {
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  const RowArgs p = p_arg;
+  pin_sgprs(p);
+  constexpr int kSteps = 9 * CG;
+  constexpr int kChunks = (kSteps + 1) / 2;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
+  const int tn = int(blockIdx.x) - rest * p.tiles_n;
+  const int b = int(fast_div(uint32_t(rest), p.div_blocks));
+  const int q = rest - b * p.blocks;
+  const int oy0 = int((int64_t(q) * p.out_h) / p.blocks);
+  const int rows_out = int((int64_t(q + 1) * p.out_h) / p.blocks) - oy0;
+  const int tile_n = tn * 64 * FN;
+
+  const int8_t *bias_lds = smem + wave * 256;
+  stage_bias<FN>(p.bias, p.gemm_n, tile_n + wave * 16 * FN, bias_lds, lane);
+
+  // padded input rows oy0 .. oy0 + rows_out + 1 of image b
+  const int8_t *rows = smem + kHaloBiasLds;
+  copy_input_rows(make_desc(p.x, p.x_bytes), lds_addr(rows), b * p.hp + oy0, rows_out + 2, wave,
+                  lane, p.row_copies, p.div_row_copies, p.row_bytes, p.div_hp, p.hp, p.units,
+                  p.div_units, p.n, p.h, p.wd, p.c, p.pad_h, p.pad_w);
+
+  FilterRing<FN, kSteps> ring;
+  ring.wd = make_desc(p.w, p.w_bytes);
+  ring.ptr = rows + p.input_bytes;
+  ring.lds = lds_addr(ring.ptr);
+  ring.slots = p.ring;
+  ring.cur = 0;
+  ring.wave = wave;
+  ring.lane = lane;
+  ring.init(tile_n, p.gemm_n, p.gemm_k);
+  for (int c = 0; c < ring.slots && c < kChunks; ++c) ring.issue(c, c);
+
+  RowState<FN, CG, NFR> st;
+#pragma unroll
+  for (int fx = 0; fx < 3; ++fx)
+#pragma unroll
+    for (int j = 0; j < NFR; ++j) {
+      // columns past the padded row (read only for dropped lanes) are clamped
+      const int col = min(16 * j + (lane & 15) + fx, p.wp - 1);
+      st.colofs[fx][j] = col * p.pitch + 16 * (lane >> 4);
+    }
+  const int m_row0 = (b * p.out_h + oy0) * p.out_w;
+
+  // Input row ir feeds output rows ir - fy (fy = 0, 1, 2) that exist:
+  // row 0 only fy = 0, row 1 fy <= 1, rows 2 .. rows_out - 1 all three, row
+  // rows_out fy >= 1 and row rows_out + 1 only fy = 2.  The first rows need
+  // only the filter rows fy <= ir, so the chunks holding taps fy = 0 (k-steps
+  // [0, 3*CG)), fy = 1 and fy = 2 are taken just before rows 0, 1 and 2;
+  // taking chunk 0 also publishes the input rows (its barrier).
+  constexpr int kC1 = (3 * CG + 1) / 2, kC2 = (6 * CG + 1) / 2;
+#define I8_ROW(K, MASK, CHECK, IR)                                                         \
+  row_step<FN, CG, NFR, K, MASK, CHECK>(p, st, frag, rows, bias_lds, IR, rows_out, m_row0, \
+                                        tile_n, wave, lane)
+  take_chunks<FN, CG, NFR, 0, kC1>(ring, st);
+  v4i frag[3][NFR];
+#pragma unroll
+  for (int fx = 0; fx < 3; ++fx)
+#pragma unroll
+    for (int j = 0; j < NFR; ++j)
+      frag[fx][j] = *reinterpret_cast<const v4i *>(rows + st.colofs[fx][j]);
+  if (rows_out < 2) {
+    // one output row: input rows 0, 1, 2 with run-time checks
+    I8_ROW(0, 1, true, 0);
+    take_chunks<FN, CG, NFR, kC1, kC2>(ring, st);
+    I8_ROW(1, 3, true, 1);
+    take_chunks<FN, CG, NFR, kC2, kChunks>(ring, st);
+    I8_ROW(2, 7, true, 2);
+    return;
+  }
+  I8_ROW(0, 1, false, 0);
+  take_chunks<FN, CG, NFR, kC1, kC2>(ring, st);
+  I8_ROW(1, 3, false, 1);
+  take_chunks<FN, CG, NFR, kC2, kChunks>(ring, st);
+  int ir = 2;
+  for (; ir + 2 < rows_out; ir += 3) {
+    I8_ROW(2, 7, false, ir);
+    I8_ROW(0, 7, false, ir + 1);
+    I8_ROW(1, 7, false, ir + 2);
+  }
+  // 0 to 2 full rows left, then the two rows that only finish earlier ones
+  switch (rows_out - ir) {
+    case 2:
+      I8_ROW(2, 7, false, ir);
+      I8_ROW(0, 7, false, ir + 1);
+      I8_ROW(1, 6, false, ir + 2);
+      I8_ROW(2, 4, false, ir + 3);
+      break;
+    case 1:
+      I8_ROW(2, 7, false, ir);
+      I8_ROW(0, 6, false, ir + 1);
+      I8_ROW(1, 4, false, ir + 2);
+      break;
+    default:
+      I8_ROW(2, 6, false, ir);
+      I8_ROW(0, 4, false, ir + 1);
+      break;
+  }
+#undef I8_ROW
+}
+
+template <int FN, int CG, int NFR>
+int launch_t(const RowArgs &h, size_t blocks, size_t lds, hipStream_t s) {
+  auto kern = row_kernel<FN, CG, NFR>;
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             int(lds));
+    if (e != hipSuccess) {
+      set_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+      return I8CONV_HIP_ERROR;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(kThreads), lds, s, h);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error(std::string("row kernel launch: ") + hipGetErrorString(e));
+    return I8CONV_HIP_ERROR;
+  }
+  return I8CONV_OK;
+}
+
+}  // namespace
+
+bool row_instance_exists(int fn, int cg, int nfr) {
+  // (the register budget of 512 per lane caps cg * nfr: the filter slice is
+  // 9 * cg * fn fragments and each input row holds 3 * nfr of them twice)
+  if (nfr < 1 || nfr > 4 || fn * nfr > 4) return false;
+  return (fn == 2 && (cg == 1 || cg == 2)) ||
+         (fn == 1 && (cg == 1 || cg == 2 || (cg == 4 && nfr <= 2)));
+}
+
+int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream) {
+  const int fn = p.bn / 64;
+  const int cg = a.c / 64;
+  const int nfr = (a.out_w + 15) / 16;
+  const HaloRowLayout row = halo_row_layout(a.wd + 2 * a.pad_w, a.c);
+  const size_t lds = size_t(kHaloBiasLds) + size_t(p.rows) * size_t(row.row_bytes) +
+                     size_t(p.ring) * halo_ring_slot_bytes(fn);
+  if (a.r != 3 || a.s != 3 || a.stride_h != 1 || a.stride_w != 1 || a.dil_h != 1 ||
+      a.dil_w != 1 || a.c % 64 != 0 || !row_instance_exists(fn, cg, nfr) ||
+      lds > size_t(kLdsBudget) || p.ranges < 1 || p.rows < 3 || p.ring < 1 ||
+      p.ring > kHaloRing || a.wd + 2 * a.pad_w != a.out_w + 2) {
+    set_error("row plan out of range");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  RowArgs h{};
+  h.x = a.x;
+  h.w = a.w;
+  h.bias = a.bias;
+  h.y = a.y;
+  h.x_bytes = a.x_bytes;
+  h.w_bytes = a.w_bytes;
+  h.n = a.n;
+  h.h = a.h;
+  h.wd = a.wd;
+  h.c = a.c;
+  h.pad_h = a.pad_h;
+  h.pad_w = a.pad_w;
+  h.out_h = a.out_h;
+  h.out_w = a.out_w;
+  h.gemm_n = a.gemm_n;
+  h.gemm_k = a.gemm_k;
+  h.hp = a.h + 2 * a.pad_h;
+  h.wp = a.wd + 2 * a.pad_w;
+  h.pitch = a.c + 16;
+  h.units = int(row.units);
+  h.row_copies = int(row.row_copies);
+  h.row_bytes = int(row.row_bytes);
+  h.input_bytes = p.rows * h.row_bytes;
+  h.blocks = p.ranges;
+  h.ring = p.ring;
+  h.tiles_n = p.tiles_n;
+  h.div_hp = make_fastdiv(uint32_t(h.hp));
+  h.div_units = make_fastdiv(uint32_t(h.units));
+  h.div_row_copies = make_fastdiv(uint32_t(h.row_copies));
+  h.div_blocks = make_fastdiv(uint32_t(h.blocks));
+  h.div_tiles_n = make_fastdiv(uint32_t(h.tiles_n));
+  const size_t grid = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define I8_ROW_CASE(FN, CG, NFR) \
+  if (fn == FN && cg == CG && nfr == NFR) return launch_t<FN, CG, NFR>(h, grid, lds, s);
+  I8_ROW_CASE(2, 1, 1) I8_ROW_CASE(2, 1, 2) I8_ROW_CASE(2, 2, 1) I8_ROW_CASE(2, 2, 2)
+  I8_ROW_CASE(1, 1, 1) I8_ROW_CASE(1, 1, 2) I8_ROW_CASE(1, 1, 3) I8_ROW_CASE(1, 1, 4)
+  I8_ROW_CASE(1, 2, 1) I8_ROW_CASE(1, 2, 2) I8_ROW_CASE(1, 2, 3) I8_ROW_CASE(1, 2, 4)
+  I8_ROW_CASE(1, 4, 1) I8_ROW_CASE(1, 4, 2)
+#undef I8_ROW_CASE
+  set_error("no row-kernel instance for this plan");
+  return I8CONV_BAD_ARGUMENT;
+}
+
+}  // namespace i8conv

@@ -186,6 +186,46 @@ bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p
   return false;
 }
 
+// Row-streaming plan (kernel_row.hip): 3x3, stride 1, dilation 1, c % 64.
+// Output rows of each image are cut into `blocks` near-equal blocks so the
+// grid (n * blocks * tiles_n workgroups) covers the 256 compute units; a
+// block's padded input rows (its rows plus two) must fit in LDS beside the
+// filter ring.
+bool plan_row(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
+  if (!(s.r == 3 && s.s == 3 && s.stride_h == 1 && s.stride_w == 1 && s.dilation_h == 1 &&
+        s.dilation_w == 1 && s.c % 64 == 0))
+    return false;
+  const int cg = s.c / 64;
+  const int nfr = int(ceil_div(g.out_w, 16));
+  const int fn = (s.k > 64 && row_instance_exists(2, cg, nfr)) ? 2 : 1;
+  if (!row_instance_exists(fn, cg, nfr)) return false;
+  const int tiles_n = int(ceil_div(s.k, 64 * fn));
+  const HaloRowLayout row = halo_row_layout(int64_t(s.w) + 2 * s.pad_w, s.c);
+  const int64_t chunks = ceil_div(g.gemm_k, 128);
+  const int64_t slot = int64_t(halo_ring_slot_bytes(fn));
+  int64_t blocks = std::min<int64_t>(g.out_h, std::max<int64_t>(1, ceil_div(256, int64_t(s.n) * tiles_n)));
+  for (; blocks <= g.out_h; ++blocks) {
+    const int64_t rows = ceil_div(g.out_h, blocks) + 2;
+    const int64_t input_lds = kHaloBiasLds + rows * row.row_bytes;
+    if (input_lds >= kLdsBudget) continue;
+    const int64_t ring = std::min<int64_t>({kHaloRing, chunks, (kLdsBudget - input_lds) / slot});
+    if (ring < 1) continue;
+    if (int64_t(s.n) * blocks * tiles_n > INT32_MAX) return false;
+    *p = PatchPlan{};
+    p->row = true;
+    p->bn = 64 * fn;
+    p->tiles_n = tiles_n;
+    p->ranges = int(blocks);
+    p->rows = int(rows);
+    p->ring = int(ring);
+    p->frags_m = nfr;
+    p->tiles_y = p->tiles_x = 1;
+    p->stage_pixels = int(rows * (s.w + 2 * s.pad_w));
+    return true;
+  }
+  return false;
+}
+
 bool finish_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
                        PatchMode mode, PatchPlan *p) {
   (void)mode;
@@ -255,7 +295,7 @@ bool search_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
 bool plan_halo(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
   if (s.c % 64 != 0) return false;
   const int bn = s.k > 64 ? 128 : 64;
-  if (plan_resident(s, g, p))
+  if (plan_row(s, g, p) || plan_resident(s, g, p))
     return true;
   return search_patch_plan(s, g, PatchMode::kStagedHalo, bn, p);
 }
