@@ -63,7 +63,7 @@ int i8conv_eligible(int id, const i8conv_shape *shape) {
     case I8CONV_KERNEL_GENERIC: return 1;
     case I8CONV_KERNEL_STRIP: return plan_strip(*shape, g, &pp) ? 1 : 0;
     case I8CONV_KERNEL_HALO: return plan_halo(*shape, g, &pp) ? 1 : 0;
-    case I8CONV_KERNEL_SPLITK: return plan_generic(g).stages >= 2 ? 1 : 0;
+    case I8CONV_KERNEL_SPLITK: return plan_generic(*shape, g).stages >= 2 ? 1 : 0;
     default: return 0;
   }
 }
@@ -72,7 +72,7 @@ size_t i8conv_workspace_bytes(int id, const i8conv_shape *shape) {
   if (id != I8CONV_KERNEL_SPLITK || !i8conv_eligible(id, shape)) return 0;
   i8conv_geometry g;
   derive(*shape, &g);
-  return splitk_workspace_bytes(g, plan_splitk(g));
+  return splitk_workspace_bytes(g, plan_splitk(*shape, g));
 }
 
 int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
@@ -86,8 +86,9 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
   std::string d;
   auto tiles = [](int64_t a, int64_t b) { return std::to_string((a + b - 1) / b); };
   if (id == I8CONV_KERNEL_GENERIC || id == I8CONV_KERNEL_SPLITK) {
-    const GemmPlan p = id == I8CONV_KERNEL_GENERIC ? plan_generic(g) : plan_splitk(g);
-    d = std::string(kNames[id]) + " tile " + std::to_string(p.bm) + "px x " +
+    const GemmPlan p = id == I8CONV_KERNEL_GENERIC ? plan_generic(*shape, g) : plan_splitk(*shape, g);
+    d = std::string(kNames[id]) + (p.dma ? " pipelined" : " register-staged") + " tile " +
+        std::to_string(p.bm) + "px x " +
         std::to_string(p.bn) + "oc, grid " + tiles(g.gemm_m, p.bm) + "x" +
         tiles(g.gemm_n, p.bn) + (p.splits > 1 ? "x" + std::to_string(p.splits) + " splits" : "") +
         ", " + std::to_string(p.stages) + " k-stages";
@@ -162,7 +163,7 @@ int i8conv_launch(int id, const i8conv_shape *shape, const int8_t *input,
   const ConvArgs args = make_args(*shape, g, input, filter, bias, output);
   switch (id) {
     case I8CONV_KERNEL_GENERIC:
-      return launch_gemm(args, plan_generic(g), stream);
+      return launch_gemm(args, plan_generic(*shape, g), stream);
     case I8CONV_KERNEL_STRIP:
     case I8CONV_KERNEL_HALO: {
       PatchPlan pp;
@@ -181,7 +182,7 @@ int i8conv_launch(int id, const i8conv_shape *shape, const int8_t *input,
         set_error("splitk needs at least two 128-byte k stages");
         return I8CONV_INELIGIBLE;
       }
-      const GemmPlan p = plan_splitk(g);
+      const GemmPlan p = plan_splitk(*shape, g);
       const size_t need = splitk_workspace_bytes(g, p);
       if (!workspace || workspace_bytes < need || !aligned(workspace, 16)) {
         set_error("splitk needs a 16-byte aligned workspace of " +

@@ -28,10 +28,14 @@ struct GemmPlan {
   int splits = 1;            // > 1 only for split-K
   int stages = 0;            // ceil(gemm_k / 128)
   int stages_per_split = 0;
+  // c % 128 == 0: the LDS-DMA pipelined kernel (kernel_gemm_dma.hip), else
+  // the register-staged one (kernel_gemm.hip)
+  bool dma = false;
 };
 bool gemm_tile_supported(int bm, int bn);
-GemmPlan plan_generic(const i8conv_geometry &g);
-GemmPlan plan_splitk(const i8conv_geometry &g);
+bool gemm_dma_tile_supported(int bm, int bn);
+GemmPlan plan_generic(const i8conv_shape &s, const i8conv_geometry &g);
+GemmPlan plan_splitk(const i8conv_shape &s, const i8conv_geometry &g);
 size_t splitk_workspace_bytes(const i8conv_geometry &g, const GemmPlan &p);
 
 // ---- halo / strip ----------------------------------------------------------
@@ -72,6 +76,8 @@ ConvArgs make_args(const i8conv_shape &s, const i8conv_geometry &g,
 int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream);
 int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
                   void *stream);
+// kernel_gemm_dma.hip; splits > 1 writes partial sums to a.partial
+int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stream);
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream);

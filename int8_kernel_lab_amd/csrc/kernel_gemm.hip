@@ -264,6 +264,7 @@ int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream) {
   args.partial = nullptr;
   args.splits = 1;
   args.stages_per_split = p.stages;
+  if (p.dma) return launch_gemm_dma(args, p, 1, stream);
   return launch_any(args, p, 1, static_cast<hipStream_t>(stream));
 }
 
@@ -274,7 +275,7 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
   args.partial = static_cast<int32_t *>(workspace);
   args.splits = p.splits;
   args.stages_per_split = p.stages_per_split;
-  int rc = launch_any(args, p, p.splits, s);
+  int rc = p.dma ? launch_gemm_dma(args, p, p.splits, stream) : launch_any(args, p, p.splits, s);
   if (rc != I8CONV_OK) return rc;
   const size_t total = size_t(a.gemm_m) * size_t(a.gemm_n);
   const bool vec = (a.gemm_n & 3) == 0 &&

@@ -16,7 +16,7 @@ namespace i8conv {
 int dispatch(const i8conv_shape &s) {
   i8conv_geometry g;
   if (derive(s, &g) != I8CONV_OK) return -1;
-  const GemmPlan gp = plan_generic(g);
+  const GemmPlan gp = plan_generic(s, g);
   const int64_t tiles = ((g.gemm_m + gp.bm - 1) / gp.bm) *
                         ((int64_t(g.gemm_n) + gp.bn - 1) / gp.bn);
   if (tiles < 128 && gp.stages >= 16) return I8CONV_KERNEL_SPLITK;

@@ -74,12 +74,28 @@ bool gemm_tile_supported(int bm, int bn) {
   }
 }
 
-// Generic tile choice: the output-channel tile is the smallest supported
-// width covering N (32/64/128 columns, 128 for wider layers); the pixel
-// tile shrinks from 256 until the grid has enough workgroups to cover the
-// 256 compute units.
-GemmPlan plan_generic(const i8conv_geometry &g) {
+// The LDS-DMA pipelined kernel (kernel_gemm_dma.hip) needs every 128-byte
+// k-stage inside one filter tap: c % 128 == 0.
+static bool dma_eligible(const i8conv_shape &s) { return s.c % kStageBytes == 0; }
+
+// Generic tile choice.  Pipelined kernel: 128 output channels per tile
+// (64 when N <= 64), and 256 pixels when that still gives the grid about
+// three quarters of the 256 compute units, else 128.  Register-staged
+// kernel: the smallest supported width covering N (32/64/128 columns, 128
+// for wider layers); the pixel tile shrinks from 256 until the grid has
+// enough workgroups to cover the 256 compute units.
+GemmPlan plan_generic(const i8conv_shape &s, const i8conv_geometry &g) {
   GemmPlan p;
+  p.stages = int(ceil_div(g.gemm_k, kStageBytes));
+  p.splits = 1;
+  p.stages_per_split = p.stages;
+  if (dma_eligible(s)) {
+    p.dma = true;
+    p.bn = g.gemm_n <= 64 ? 64 : 128;
+    const int64_t tiles_n = ceil_div(g.gemm_n, p.bn);
+    p.bm = ceil_div(g.gemm_m, 256) * tiles_n >= 192 ? 256 : 128;
+    return p;
+  }
   p.bn = g.gemm_n <= 32 ? 32 : (g.gemm_n <= 64 ? 64 : 128);
   const int64_t tiles_n = ceil_div(g.gemm_n, p.bn);
   p.bm = 64;
@@ -91,22 +107,27 @@ GemmPlan plan_generic(const i8conv_geometry &g) {
     }
   }
   if (!gemm_tile_supported(p.bm, p.bn)) p.bm = 128;
-  p.stages = int(ceil_div(g.gemm_k, kStageBytes));
-  p.splits = 1;
-  p.stages_per_split = p.stages;
   return p;
 }
 
-// Split-K: the generic tile, with the 128-byte k stages divided among
-// enough splits to give about two workgroups per compute unit.
-GemmPlan plan_splitk(const i8conv_geometry &g) {
+// Split-K: a 128-pixel tile (64 for tiny M on the register-staged kernel),
+// with the 128-byte k stages divided among enough splits to give about one
+// workgroup per compute unit (pipelined kernel: its LDS ring allows one per
+// unit) or two (register-staged).
+GemmPlan plan_splitk(const i8conv_shape &s, const i8conv_geometry &g) {
   GemmPlan p;
-  p.bn = g.gemm_n <= 32 ? 32 : (g.gemm_n <= 64 ? 64 : 128);
-  p.bm = g.gemm_m <= 64 ? 64 : 128;
-  if (!gemm_tile_supported(p.bm, p.bn)) p.bm = 128;
   p.stages = int(ceil_div(g.gemm_k, kStageBytes));
+  p.dma = dma_eligible(s);
+  if (p.dma) {
+    p.bn = g.gemm_n <= 64 ? 64 : 128;
+    p.bm = 128;
+  } else {
+    p.bn = g.gemm_n <= 32 ? 32 : (g.gemm_n <= 64 ? 64 : 128);
+    p.bm = g.gemm_m <= 64 ? 64 : 128;
+    if (!gemm_tile_supported(p.bm, p.bn)) p.bm = 128;
+  }
   const int64_t tiles = ceil_div(g.gemm_m, p.bm) * ceil_div(g.gemm_n, p.bn);
-  int64_t splits = ceil_div(512, tiles);
+  int64_t splits = ceil_div(p.dma ? 256 : 512, tiles);
   splits = std::max<int64_t>(2, std::min<int64_t>(splits, p.stages));
   p.stages_per_split = int(ceil_div(p.stages, splits));
   p.splits = int(ceil_div(p.stages, p.stages_per_split));
