@@ -160,16 +160,18 @@ __device__ __forceinline__ v4i load_bias4(const int32_t *base, int count, int i0
   return v;
 }
 
-// Final-output stores.  Non-temporal: the int32 output of a layer is several
-// times larger than its int8 input and filter, and written once, so it is
-// streamed through the L2 with the evict-first policy instead of pushing
-// the input rows and filter (read by every workgroup) out of it.
+// Final-output stores.  16-byte stores are non-temporal: the int32 output of
+// a layer is several times larger than its int8 input and filter, and
+// written once, so it is streamed through the L2 with the evict-first
+// policy instead of pushing the input rows and filter (read by every
+// workgroup) out of it.  The 4-byte stores of a channel tail (N % 4 != 0)
+// stay ordinary: each covers a sliver of a line, and only ordinary stores
+// are merged into whole lines in the L2 (non-temporal ones went to HBM as
+// partial writes and made such layers several times slower).
 __device__ __forceinline__ void store_out4(int32_t *dst, v4i v) {
   __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst));
 }
-__device__ __forceinline__ void store_out1(int32_t *dst, int32_t v) {
-  __builtin_nontemporal_store(v, dst);
-}
+__device__ __forceinline__ void store_out1(int32_t *dst, int32_t v) { *dst = v; }
 
 // D = A x B + C over int8 -> int32.  A is 16 rows (lane % 16) by 64 k,
 // B is 64 k by 16 columns (lane % 16); lane l supplies 16 k-bytes of its

@@ -2,13 +2,22 @@
 // README.md:92-99: sweep, then encode the policy outside the kernels while
 // eligibility stays an explicit predicate next to each kernel).
 //
-// The policy only ever returns an eligible kernel.  Its rules:
-//   1. split-K when the generic grid cannot fill the chip (fewer than 128
-//      workgroups) and the reduction is long (>= 16 stages of 128 k-bytes),
-//      e.g. a 7x7 layer with C = 2048;
-//   2. otherwise an input-reuse kernel for a spatial filter (r*s > 1):
-//      halo when eligible, else strip;
-//   3. otherwise the generic implicit GEMM (1x1 layers, C % 64 != 0).
+// The policy only ever returns an eligible kernel.  Its rules, in order,
+// read off a sweep of the reference's 41-layer table on one MI355X:
+//   1. the row-streaming 3x3 stride-1 kernel (a halo plan) whenever it has a
+//      plan: it won every layer it covers (ResNet/Darknet 3x3 stages,
+//      batched 56x56 and 28x28 layers, 14x14 C = 256);
+//   2. split-K when the generic grid cannot fill the chip (fewer than 128
+//      tiles) and the reduction is long (>= 16 stages of 128 k-bytes): deep
+//      7x7 / 13x13 / 14x14 layers and stride-2 downsamplers at batch 1;
+//   3. the pipelined generic GEMM (C % 128 == 0) when its grid has at least
+//      128 tiles: large layers of any filter (it beat every halo/strip plan
+//      from 28x28 x 32 images up to 256x256 x 16, stride 1 or 2, 3x3 or 5x5,
+//      dilated or not);
+//   4. otherwise an input-reuse kernel for a spatial filter (r*s > 1): halo
+//      when eligible, else strip (small dilated layers, asymmetric 1x3/3x1,
+//      C = 64 layers wider than the row kernel's four fragments);
+//   5. otherwise the generic implicit GEMM (1x1 layers, C % 64 != 0).
 #include "i8conv_internal.hpp"
 
 namespace i8conv {
@@ -16,13 +25,16 @@ namespace i8conv {
 int dispatch(const i8conv_shape &s) {
   i8conv_geometry g;
   if (derive(s, &g) != I8CONV_OK) return -1;
+  PatchPlan pp;
+  const bool halo = plan_halo(s, g, &pp);
+  if (halo && pp.row) return I8CONV_KERNEL_HALO;
   const GemmPlan gp = plan_generic(s, g);
   const int64_t tiles = ((g.gemm_m + gp.bm - 1) / gp.bm) *
                         ((int64_t(g.gemm_n) + gp.bn - 1) / gp.bn);
   if (tiles < 128 && gp.stages >= 16) return I8CONV_KERNEL_SPLITK;
+  if (gp.dma && tiles >= 128) return I8CONV_KERNEL_GENERIC;
   if (int64_t(s.r) * s.s > 1) {
-    PatchPlan pp;
-    if (plan_halo(s, g, &pp)) return I8CONV_KERNEL_HALO;
+    if (halo) return I8CONV_KERNEL_HALO;
     if (plan_strip(s, g, &pp)) return I8CONV_KERNEL_STRIP;
   }
   return I8CONV_KERNEL_GENERIC;

@@ -150,11 +150,11 @@ BASELINE_TABLE_EXPECTED = {
     # name: (strip, halo, dispatch)
     "cfg1_smoke": (True, True, "halo"),
     "cfg2_resnet_3x3_s1": (True, True, "halo"),
-    "cfg3_down_3x3_s2": (False, True, "halo"),
+    "cfg3_down_3x3_s2": (False, True, "generic"),
     "cfg4a_pointwise_1x1": (False, True, "generic"),
     "cfg4b_k36_tail": (True, True, "halo"),
     "cfg5a_deep_k": (True, True, "splitk"),
-    "cfg5b_dilated": (False, True, "halo"),
+    "cfg5b_dilated": (False, True, "generic"),
 }
 
 
