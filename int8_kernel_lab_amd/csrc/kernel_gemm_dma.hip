@@ -23,7 +23,8 @@
 //     128 workgroup tile runs eight waves, two per SIMD, so one wave's MFMAs
 //     run while the other waits on its copies or fragment reads, and twice
 //     as many copies are in flight per compute unit;
-//   * accumulators stay in VGPRs (built with -amdgpu-mfma-vgpr-form).
+//   * accumulators stay in VGPRs (built with -amdgpu-mfma-vgpr-form);
+//   * XCD-aware tile order (see below).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -63,9 +64,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(ConvArgs a) {
   const int wm = wave % WM;
   const int wn = wave / WM;
 
+  // Workgroup i runs on XCD i % 8 (round-robin dispatch), and each XCD has
+  // its own L2.  Tiles are handed out so that every XCD gets a contiguous
+  // run of them (both channel tiles of a pixel tile, then the next pixel
+  // tile): neighbouring pixel tiles share input rows, which then stay in
+  // that XCD's L2 instead of being fetched into two.  A bijection on
+  // [0, gridDim.x): the first 8 * (gridDim.x / 8) workgroups are permuted,
+  // the rest keep their index.
+  const int per_xcd = int(gridDim.x) / 8;
+  int tile = int(blockIdx.x);
+  if (tile < 8 * per_xcd) tile = (tile % 8) * per_xcd + tile / 8;
   const int tiles_n = (a.gemm_n + BN - 1) / BN;
-  const int tile_m = int(blockIdx.x / tiles_n) * BM;
-  const int tile_n = int(blockIdx.x % tiles_n) * BN;
+  const int tile_m = (tile / tiles_n) * BM;
+  const int tile_n = (tile % tiles_n) * BN;
   const int stages = a.gemm_k / kStageBytes;
   int s_begin = 0, s_end = stages;
   if (kSplit) {
