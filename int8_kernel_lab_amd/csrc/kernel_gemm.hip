@@ -200,15 +200,30 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(ConvArgs a) {
 // order.  Vector form: four consecutive channels per thread (N % 4 == 0).
 __global__ __launch_bounds__(kThreads) void splitk_reduce_vec(
     const int32_t *__restrict__ partial, const int32_t *__restrict__ bias,
-    int32_t *__restrict__ y, int gemm_n, size_t total4, int splits) {
-  const size_t total = total4 * 4;
-  for (size_t q = size_t(blockIdx.x) * kThreads + threadIdx.x; q < total4;
-       q += size_t(gridDim.x) * kThreads) {
-    const int oc = int((q * 4) % size_t(gemm_n));
-    v4i acc = v4i{bias[oc], bias[oc + 1], bias[oc + 2], bias[oc + 3]};
-    for (int s = 0; s < splits; ++s)
-      acc = add_wrap(acc, *reinterpret_cast<const v4i *>(partial + size_t(s) * total + q * 4));
-    *reinterpret_cast<v4i *>(y + q * 4) = acc;
+    int32_t *__restrict__ y, int n4, size_t total4, int splits) {
+  // Each thread walks vec4 items q, q + G, ... (G threads in the grid); its
+  // channel group q mod n4 is found once and then advanced by G mod n4,
+  // so the loop has no 64-bit division.  The splits are added eight loads
+  // at a time (all in flight together), still in split order.
+  const size_t grid = size_t(gridDim.x) * kThreads;
+  const int step4 = int(grid % size_t(n4));
+  size_t q = size_t(blockIdx.x) * kThreads + threadIdx.x;
+  int c4 = int(q % size_t(n4));
+  for (; q < total4; q += grid) {
+    const v4i *src = reinterpret_cast<const v4i *>(partial) + q;
+    v4i acc = reinterpret_cast<const v4i *>(bias)[c4];
+    int sp = 0;
+    for (; sp + 8 <= splits; sp += 8) {
+      v4i t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = src[size_t(sp + u) * total4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = add_wrap(acc, t[u]);
+    }
+    for (; sp < splits; ++sp) acc = add_wrap(acc, src[size_t(sp) * total4]);
+    reinterpret_cast<v4i *>(y)[q] = acc;
+    c4 += step4;
+    if (c4 >= n4) c4 -= n4;
   }
 }
 
@@ -281,14 +296,14 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
   const bool vec = (a.gemm_n & 3) == 0 &&
                    (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
-                   (reinterpret_cast<uintptr_t>(a.bias) & 3) == 0;
+                   (reinterpret_cast<uintptr_t>(a.bias) & 15) == 0;
   const size_t work = vec ? total / 4 : total;
   size_t blocks = (work + kThreads - 1) / kThreads;
   if (blocks > 4096) blocks = 4096;
   if (blocks == 0) blocks = 1;
   if (vec) {
     hipLaunchKernelGGL(splitk_reduce_vec, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
-                       args.partial, a.bias, a.y, a.gemm_n, total / 4, p.splits);
+                       args.partial, a.bias, a.y, a.gemm_n / 4, total / 4, p.splits);
   } else {
     hipLaunchKernelGGL(splitk_reduce_scalar, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
                        args.partial, a.bias, a.y, a.gemm_n, total, p.splits);

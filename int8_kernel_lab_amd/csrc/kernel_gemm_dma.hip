@@ -19,10 +19,10 @@
 //   * because a stage lies inside one tap, the tap decomposition is uniform
 //     per stage: each lane keeps its rows' pixel origin and adds one tap
 //     offset per stage, with two compares for padding;
-//   * 64 x 64 wave tiles (64 x 32 for the narrow 128 x 64 tile); the 256 x
-//     128 workgroup tile runs eight waves, two per SIMD, so one wave's MFMAs
-//     run while the other waits on its copies or fragment reads, and twice
-//     as many copies are in flight per compute unit;
+//   * eight waves, two per SIMD, on the 256 x 128, 256 x 64 and 128 x 128
+//     tiles (wave tiles 64 x 64 or 64 x 32), so one wave's MFMAs run while
+//     the other waits on its copies or fragment reads, and twice as many
+//     copies are in flight per compute unit; four on the small 128 x 64 tile;
 //   * accumulators stay in VGPRs (built with -amdgpu-mfma-vgpr-form);
 //   * XCD-aware tile order (see below).
 #include <hip/hip_runtime.h>
@@ -293,12 +293,12 @@ int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stre
     set_error("pipelined gemm plan out of range");
     return I8CONV_BAD_ARGUMENT;
   }
-  // wave tiles of 64 pixels x 64 channels (x 32 for the narrow tile); the
-  // 256 x 128 tile runs eight waves, two per SIMD
+  // eight waves, two per SIMD (wave tiles 64 x 64, or 64 x 32 on the
+  // narrower tiles), except the small 128 x 64 tile
   switch (p.bm * 1000 + p.bn) {
     case 128064: return launch_tile<128, 64, 2, 2>(a, splits, s);
-    case 128128: return launch_tile<128, 128, 2, 2>(a, splits, s);
-    case 256064: return launch_tile<256, 64, 4, 1>(a, splits, s);
+    case 128128: return launch_tile<128, 128, 2, 4>(a, splits, s);
+    case 256064: return launch_tile<256, 64, 4, 2>(a, splits, s);
     case 256128: return launch_tile<256, 128, 4, 2>(a, splits, s);
   }
   set_error("unsupported pipelined gemm tile");
