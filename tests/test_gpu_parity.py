@@ -46,6 +46,17 @@ EDGE = {
     "k300": lab.ConvShape(1, 8, 8, 64, 300, 3, 3, 1, 1, 1, 1, 1, 1),
     "m_tail": lab.ConvShape(3, 7, 9, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "s2_dil2": lab.ConvShape(2, 30, 30, 64, 64, 3, 3, 2, 2, 2, 2, 2, 2),
+    # c % 128 == 0: the LDS-DMA pipelined generic / split-K kernel.  Channel
+    # tails with N % 4 != 0 (scalar stores and the scalar reduce), pixel
+    # tails, stride + dilation + asymmetric padding, a grid of tiles that is
+    # not a multiple of the 8 XCDs, one k-stage per tap and several.
+    "dma_k38_tails": lab.ConvShape(3, 11, 13, 128, 38, 3, 3, 1, 1, 1, 1, 1, 1),
+    "dma_k198_s2_dil2": lab.ConvShape(2, 23, 21, 256, 198, 3, 3, 2, 1, 2, 2, 2, 1),
+    "dma_1x1_m_tail": lab.ConvShape(5, 17, 19, 384, 96, 1, 1, 0, 0, 1, 1, 1, 1),
+    "dma_5x3_asym": lab.ConvShape(1, 40, 36, 128, 136, 5, 3, 2, 0, 1, 2, 1, 3),
+    "dma_grid_9x2": lab.ConvShape(1, 48, 48, 128, 200, 3, 3, 1, 1, 1, 1, 1, 1),
+    "dma_256x128_tails": lab.ConvShape(4, 63, 99, 128, 134, 3, 3, 1, 1, 1, 1, 1, 1),
+    "dma_256x64_tails": lab.ConvShape(16, 56, 55, 256, 62, 1, 1, 0, 0, 1, 1, 1, 1),
 }
 
 _expected_cache = {}
