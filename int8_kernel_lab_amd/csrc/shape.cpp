@@ -218,33 +218,47 @@ bool plan_row(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
     return false;
   const int cg = s.c / 64;
   const int nfr = int(ceil_div(g.out_w, 16));
-  const int fn = (s.k > 64 && row_instance_exists(2, cg, nfr)) ? 2 : 1;
-  if (!row_instance_exists(fn, cg, nfr)) return false;
-  const int tiles_n = int(ceil_div(s.k, 64 * fn));
   const HaloRowLayout row = halo_row_layout(int64_t(s.w) + 2 * s.pad_w, s.c);
   const int64_t chunks = ceil_div(g.gemm_k, 128);
-  const int64_t slot = int64_t(halo_ring_slot_bytes(fn));
-  int64_t blocks = std::min<int64_t>(g.out_h, std::max<int64_t>(1, ceil_div(256, int64_t(s.n) * tiles_n)));
-  for (; blocks <= g.out_h; ++blocks) {
-    const int64_t rows = ceil_div(g.out_h, blocks) + 2;
-    const int64_t input_lds = kHaloBiasLds + rows * row.row_bytes;
-    if (input_lds >= kLdsBudget) continue;
-    const int64_t ring = std::min<int64_t>({kHaloRing, chunks, (kLdsBudget - input_lds) / slot});
-    if (ring < 1) continue;
-    if (int64_t(s.n) * blocks * tiles_n > INT32_MAX) return false;
-    *p = PatchPlan{};
-    p->row = true;
-    p->bn = 64 * fn;
-    p->tiles_n = tiles_n;
-    p->ranges = int(blocks);
-    p->rows = int(rows);
-    p->ring = int(ring);
-    p->frags_m = nfr;
-    p->tiles_y = p->tiles_x = 1;
-    p->stage_pixels = int(rows * (s.w + 2 * s.pad_w));
-    return true;
+  // For each channel slice width (16*fn channels per wave), the smallest
+  // number of row blocks per image that gives every compute unit a
+  // workgroup and fits in LDS.  Among the widths with a plan, keep the one
+  // whose workgroup copies the fewest bytes (input rows + filter slice):
+  // that copy is what the workgroup waits for before its MFMAs can run.
+  bool found = false;
+  int64_t best_bytes = 0;
+  for (int fn : {2, 1}) {
+    if (fn == 2 && s.k <= 64) continue;
+    if (!row_instance_exists(fn, cg, nfr)) continue;
+    const int tiles_n = int(ceil_div(s.k, 64 * fn));
+    const int64_t slot = int64_t(halo_ring_slot_bytes(fn));
+    int64_t blocks = std::min<int64_t>(g.out_h, std::max<int64_t>(1, ceil_div(256, int64_t(s.n) * tiles_n)));
+    for (; blocks <= g.out_h; ++blocks) {
+      const int64_t rows = ceil_div(g.out_h, blocks) + 2;
+      const int64_t input_lds = kHaloBiasLds + rows * row.row_bytes;
+      if (input_lds >= kLdsBudget) continue;
+      const int64_t ring = std::min<int64_t>({kHaloRing, chunks, (kLdsBudget - input_lds) / slot});
+      if (ring < 1) continue;
+      if (int64_t(s.n) * blocks * tiles_n > INT32_MAX) break;
+      const int64_t bytes = rows * row.row_bytes + int64_t(64) * fn * g.gemm_k;
+      if (!found || bytes < best_bytes) {
+        found = true;
+        best_bytes = bytes;
+        *p = PatchPlan{};
+        p->row = true;
+        p->bn = 64 * fn;
+        p->tiles_n = tiles_n;
+        p->ranges = int(blocks);
+        p->rows = int(rows);
+        p->ring = int(ring);
+        p->frags_m = nfr;
+        p->tiles_y = p->tiles_x = 1;
+        p->stage_pixels = int(rows * (s.w + 2 * s.pad_w));
+      }
+      break;
+    }
   }
-  return false;
+  return found;
 }
 
 bool finish_patch_plan(const i8conv_shape &s, const i8conv_geometry &g,
