@@ -24,6 +24,25 @@ __device__ __forceinline__ void pin_sgprs(const T &v) {
   for (int i = 0; i < int(sizeof(T) / 4); ++i) asm volatile("" ::"s"(w[i]));
 }
 
+// s_waitcnt vmcnt(min(n, 63)) for a wave-uniform run-time n (the counter
+// field is six bits; waiting for fewer outstanding copies is always safe).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n > 63 ? 63 : n) {
+#define I8_VM(N) \
+  case N: asm volatile("s_waitcnt vmcnt(" #N ")" ::: "memory"); break;
+    I8_VM(0) I8_VM(1) I8_VM(2) I8_VM(3) I8_VM(4) I8_VM(5) I8_VM(6) I8_VM(7)
+    I8_VM(8) I8_VM(9) I8_VM(10) I8_VM(11) I8_VM(12) I8_VM(13) I8_VM(14) I8_VM(15)
+    I8_VM(16) I8_VM(17) I8_VM(18) I8_VM(19) I8_VM(20) I8_VM(21) I8_VM(22) I8_VM(23)
+    I8_VM(24) I8_VM(25) I8_VM(26) I8_VM(27) I8_VM(28) I8_VM(29) I8_VM(30) I8_VM(31)
+    I8_VM(32) I8_VM(33) I8_VM(34) I8_VM(35) I8_VM(36) I8_VM(37) I8_VM(38) I8_VM(39)
+    I8_VM(40) I8_VM(41) I8_VM(42) I8_VM(43) I8_VM(44) I8_VM(45) I8_VM(46) I8_VM(47)
+    I8_VM(48) I8_VM(49) I8_VM(50) I8_VM(51) I8_VM(52) I8_VM(53) I8_VM(54) I8_VM(55)
+    I8_VM(56) I8_VM(57) I8_VM(58) I8_VM(59) I8_VM(60) I8_VM(61) I8_VM(62)
+#undef I8_VM
+    default: asm volatile("s_waitcnt vmcnt(63)" ::: "memory"); break;
+  }
+}
+
 // The filter staging ring: chunk c = bytes [128c, 128c + 128) of the
 // workgroup's 64*FN filter rows, in ring slot c % slots.  Each wave copies
 // and reads only its own 16*FN rows of every slot, so a chunk needs no

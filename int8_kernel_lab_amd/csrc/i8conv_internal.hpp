@@ -58,6 +58,8 @@ struct PatchPlan {
   // halo, 3x3 stride 1: output-row blocks streamed row by row with the
   // taps formed in registers (kernel_row.hip); `ranges` = blocks per image
   bool row = false;
+  // row-streaming, 128 channels: the two-pass form (kernel_rowpass.hip)
+  bool pass2 = false;
   int ranges = 0;  // resident: pixel ranges per channel slice
   int rows = 0;    // resident: most padded input rows any range needs
   int ring = 0;    // resident: filter staging slots in LDS
@@ -81,6 +83,11 @@ int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stre
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream);
+int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream);
+// kernel_rowpass.hip: fragments per output row of its instance for out_w
+// (0: none), and its LDS bytes for wp padded columns and `rows` output rows
+int rowpass_nfr(int out_w);
+size_t rowpass_lds_bytes(int wp, int rows);
 // Whether kernel_row.hip has an instance for 16*fn channels per wave, cg
 // 64-channel groups and nfr 16-column fragments per output row.
 bool row_instance_exists(int fn, int cg, int nfr);
