@@ -15,7 +15,8 @@
 // filter, then the group-1 halves.  Pass 0 walks the input rows with the
 // group-0 data only and accumulates every output row of the block in
 // registers (R rows x NFR fragments); pass 1 repeats the walk with group 1
-// and completes output row ir - 2 at input row ir, which is stored at once.
+// and completes output row ir - 2 at input row ir, which is stored one
+// input row later.
 // Pass 0 needs half of the bytes, and the group-1 copies land while it runs.
 //
 // Layouts.  Input: one LDS plane per (group, padded row): wp pixels x 80
@@ -49,6 +50,7 @@ struct PassArgs {
   const int32_t *bias;
   int32_t *y;
   uint32_t x_bytes, w_bytes;
+  uint32_t y_bytes;  // output bytes (< 2^31: checked at launch)
   int n, h, wd, c, pad_h, pad_w;
   int out_h, out_w, gemm_n, gemm_k;
   int hp, wp;        // padded rows per image, padded columns
@@ -66,6 +68,13 @@ struct PassState {
   int colofs[3][NFR];      // LDS offset of this lane's column + fx / k-block in a plane
   const int8_t *planes;    // group-0 planes, then group-1 planes
   int plane_bytes;
+  // Output, vector path: a buffer resource over y, this lane's byte offset
+  // of output row 0 per fragment (out of range where the column or the
+  // channels fall outside the layer: the store is dropped, no branch), and
+  // the byte stride between output rows (a scalar offset per row).
+  __amdgpu_buffer_rsrc_t yr;
+  uint32_t voff[NFR];
+  uint32_t row_stride;
 
   __device__ __forceinline__ void load_row(const int8_t *plane) {
 #pragma unroll
@@ -78,8 +87,8 @@ struct PassState {
   // Input row IR of group G: MFMAs into output rows IR - fy (compile-time
   // valid ones); in pass 1, output row IR - 2 is then complete and stored.
   template <int G, int IR>
-  __device__ __forceinline__ void step(const PassArgs &p, const int8_t *bias_lds, int rows_out,
-                                       int m_row0, int oc0, int lane) {
+  __device__ __forceinline__ void step(const PassArgs &p, bool vec, int rows_out, int m_row0,
+                                       int oc0, int lane) {
     v4i cur[3][NFR];
 #pragma unroll
     for (int fx = 0; fx < 3; ++fx)
@@ -101,34 +110,43 @@ struct PassState {
         }
       }
     }
-    if (G == kGroups - 1 && IR >= 2) {
-      constexpr int o = IR >= 2 ? IR - 2 : 0;
-      if (o < rows_out) {
-        const v4i bv = *reinterpret_cast<const v4i *>(bias_lds + 16 * (lane >> 4));
-        const bool vec = (p.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
-        const int m_row = m_row0 + o * p.out_w;
+    // Output row IR - 2 is complete after this row's MFMAs; it is stored one
+    // row later, so that its accumulators are read long after the MFMAs that
+    // wrote them (reading them right away would stall the wave until those
+    // MFMAs drained, every row).
+    if (G == kGroups - 1 && IR >= 3)
+      store_row<(IR >= 3 ? IR - 3 : 0)>(p, vec, rows_out, m_row0, oc0, lane);
+  }
+
+  // Output row O: the accumulators already hold bias + dot products.  N % 4
+  // == 0 (and a 16-byte aligned output): one 16-byte non-temporal buffer
+  // store per fragment, no address arithmetic; otherwise element stores.
+  template <int O>
+  __device__ __forceinline__ void store_row(const PassArgs &p, bool vec, int rows_out, int m_row0,
+                                            int oc0, int lane) {
+    if (O >= rows_out) return;
+    if (vec) {
 #pragma unroll
-        for (int j = 0; j < NFR; ++j) {
-          const int col = 16 * j + (lane & 15);
-          if (col >= p.out_w) continue;
-          const v4i v = add_wrap4(acc[o][j], bv);
-          int32_t *dst = p.y + size_t(m_row + col) * size_t(p.gemm_n) + oc0;
-          if (vec) {
-            if (oc0 < p.gemm_n) store_out4(dst, v);
-          } else {
+      for (int j = 0; j < NFR; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(acc[O][j], yr, voff[j], O * row_stride, 2 /* nt */);
+      return;
+    }
+    const int m_row = m_row0 + O * p.out_w;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (oc0 + e < p.gemm_n) store_out1(dst + e, v[e]);
-          }
-        }
-      }
+    for (int j = 0; j < NFR; ++j) {
+      const int col = 16 * j + (lane & 15);
+      if (col >= p.out_w) continue;
+      int32_t *dst = p.y + size_t(m_row + col) * size_t(p.gemm_n) + oc0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (oc0 + e < p.gemm_n) store_out1(dst + e, acc[O][j][e]);
     }
   }
 
   template <int G, size_t... I>
-  __device__ __forceinline__ void pass(const PassArgs &p, const int8_t *bias_lds, int rows_out,
-                                       int m_row0, int oc0, int lane, std::index_sequence<I...>) {
-    (step<G, int(I)>(p, bias_lds, rows_out, m_row0, oc0, lane), ...);
+  __device__ __forceinline__ void pass(const PassArgs &p, bool vec, int rows_out, int m_row0,
+                                       int oc0, int lane, std::index_sequence<I...>) {
+    (step<G, int(I)>(p, vec, rows_out, m_row0, oc0, lane), ...);
   }
 };
 
@@ -219,12 +237,18 @@ __global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
       const int col = min(16 * j + (lane & 15) + fx, p.wp - 1);
       st.colofs[fx][j] = col * (16 * kUnits) + 16 * (lane >> 4);
     }
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int j = 0; j < NFR; ++j) st.acc[r][j] = v4i{0, 0, 0, 0};
   const int m_row0 = (b * p.out_h + oy0) * p.out_w;
   const int oc0 = tile_n + wave * 16 + 4 * (lane >> 4);
+  const bool vec = (p.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
+  st.yr = make_rsrc(p.y, p.y_bytes);
+  st.row_stride = uint32_t(p.out_w) * uint32_t(p.gemm_n) * 4u;
+#pragma unroll
+  for (int j = 0; j < NFR; ++j) {
+    const int col = 16 * j + (lane & 15);
+    st.voff[j] = col < p.out_w && oc0 < p.gemm_n
+                     ? (uint32_t(m_row0 + col) * uint32_t(p.gemm_n) + uint32_t(oc0)) * 4u
+                     : kOutOfRange;
+  }
 
   // Pass 0 once the bias, the group-0 planes and filter halves have landed:
   // only this wave's group-1 copies (issued after them) may be in flight.
@@ -232,13 +256,20 @@ __global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
   __syncthreads();
   take_filter(0);
   st.load_row(st.planes);
-  st.template pass<0>(p, bias_lds, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
+  // the accumulators start at the bias (the oracle adds the bias first)
+  const v4i bv = *reinterpret_cast<const v4i *>(bias_lds + 16 * (lane >> 4));
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < NFR; ++j) st.acc[r][j] = bv;
+  st.template pass<0>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
   // Pass 1: everything has landed (no store has been issued yet).
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   take_filter(1);
   st.load_row(st.planes + p.rows_in * st.plane_bytes);
-  st.template pass<1>(p, bias_lds, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
+  st.template pass<1>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
+  st.template store_row<R - 1>(p, vec, rows_out, m_row0, oc0, lane);
 }
 
 template <int R, int NFR>
@@ -285,7 +316,8 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
   if (a.r != 3 || a.s != 3 || a.stride_h != 1 || a.stride_w != 1 || a.dil_h != 1 ||
       a.dil_w != 1 || a.c != 64 * kGroups || R < 1 || R > 8 || nfr == 0 || p.bn != 64 ||
       lds > size_t(kLdsBudget) || p.ranges < 1 || wp != a.out_w + 2 ||
-      int64_t(a.out_h) > int64_t(p.ranges) * R) {
+      int64_t(a.out_h) > int64_t(p.ranges) * R ||
+      int64_t(a.gemm_m) * a.gemm_n * 4 > int64_t(INT32_MAX)) {
     set_error("two-pass row plan out of range");
     return I8CONV_BAD_ARGUMENT;
   }
@@ -296,6 +328,7 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
   h.y = a.y;
   h.x_bytes = a.x_bytes;
   h.w_bytes = a.w_bytes;
+  h.y_bytes = uint32_t(int64_t(a.gemm_m) * a.gemm_n * 4);
   h.n = a.n;
   h.h = a.h;
   h.wd = a.wd;
