@@ -91,7 +91,8 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
         std::to_string(p.bm) + "px x " +
         std::to_string(p.bn) + "oc, grid " + tiles(g.gemm_m, p.bm) + "x" +
         tiles(g.gemm_n, p.bn) + (p.splits > 1 ? "x" + std::to_string(p.splits) + " splits" : "") +
-        ", " + std::to_string(p.stages) + " k-stages";
+        ", " + std::to_string(p.stages) + " k-stages" +
+        (p.dma && gemm_dma_copy_waves(p) > 0 ? ", " + std::to_string(gemm_dma_copy_waves(p)) + " copy waves" : "");
   } else {
     PatchPlan p;
     if (id == I8CONV_KERNEL_STRIP) plan_strip(*shape, g, &p);

@@ -34,6 +34,9 @@ struct GemmPlan {
 };
 bool gemm_tile_supported(int bm, int bn);
 bool gemm_dma_tile_supported(int bm, int bn);
+// copy-only waves the pipelined kernel adds to a workgroup of this plan (0:
+// every wave copies and runs MFMAs)
+int gemm_dma_copy_waves(const GemmPlan &p);
 GemmPlan plan_generic(const i8conv_shape &s, const i8conv_geometry &g);
 GemmPlan plan_splitk(const i8conv_shape &s, const i8conv_geometry &g);
 size_t splitk_workspace_bytes(const i8conv_geometry &g, const GemmPlan &p);

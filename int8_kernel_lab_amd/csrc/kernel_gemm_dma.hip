@@ -11,7 +11,7 @@
 //     (buffer_load ... lds, 1 KB per wave instruction), no VGPR round trip;
 //   * a ring of three stage buffers: stage s + 2 is in flight while stage s
 //     feeds the MFMAs, one barrier per stage; the copies of stage s + 2 are
-//     issued between the MFMA groups of stage s;
+//     issued between the MFMA groups of stage s, or by copy waves (below);
 //   * the LDS rows use the conflict-free swz128 layout.  A copy writes lane
 //     i's 16 bytes to LDS slot i of its 1 KB block, so the swizzle is applied
 //     on the source side: the lane of slot (row, physical chunk) fetches the
@@ -19,10 +19,14 @@
 //   * because a stage lies inside one tap, the tap decomposition is uniform
 //     per stage: each lane keeps its rows' pixel origin and adds one tap
 //     offset per stage, with two compares for padding;
-//   * eight waves, two per SIMD, on the 256 x 128, 256 x 64 and 128 x 128
-//     tiles (wave tiles 64 x 64 or 64 x 32), so one wave's MFMAs run while
-//     the other waits on its copies or fragment reads, and twice as many
-//     copies are in flight per compute unit; four on the small 128 x 64 tile;
+//   * eight MFMA waves, two per SIMD, on the 256 x 128, 256 x 64 and
+//     128 x 128 tiles (wave tiles 64 x 64 or 64 x 32), so one wave's MFMAs
+//     run while the other waits on its fragment reads; four on the small
+//     128 x 64 tile;
+//   * on the 256 x 128 and 128 x 128 tiles with four or more k-stages per
+//     workgroup, four more waves that only issue the copies: an MFMA wave
+//     that also issues copies stalls whenever the buffer unit's queue is
+//     full, and its MFMAs wait behind the stalled issue;
 //   * accumulators stay in VGPRs (built with -amdgpu-mfma-vgpr-form);
 //   * XCD-aware tile order (see below).
 #include <hip/hip_runtime.h>
@@ -43,9 +47,15 @@ __device__ __forceinline__ v4i add_wrap(v4i a, v4i b) {
   return __builtin_bit_cast(v4i, __builtin_bit_cast(v4u_t, a) + __builtin_bit_cast(v4u_t, b));
 }
 
-template <int BM, int BN, int WM, int WN, bool kSplit>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(ConvArgs a) {
-  constexpr int NW = WM * WN;   // waves
+// NCW == 0: every wave both copies and runs MFMAs.  NCW > 0: WM*WN MFMA
+// waves plus NCW copy waves (waves WM*WN and up) that only issue the stage
+// copies, so an MFMA wave never stalls on a copy issue.  The two roles run
+// separate loops with the same one barrier per stage, so neither role's
+// registers are live in the other's loop.
+template <int BM, int BN, int WM, int WN, bool kSplit, int NCW>
+__global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs a) {
+  constexpr int NMW = WM * WN;             // MFMA waves
+  constexpr int NW = NCW > 0 ? NCW : NMW;  // copy waves
   constexpr int TMW = BM / WM;  // pixels per wave
   constexpr int TNW = BN / WN;  // output channels per wave
   constexpr int FM = TMW / 16;
@@ -60,7 +70,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(ConvArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool copier = NCW > 0 && wave_id >= NMW;  // a copy-only wave
+  const int wave = copier ? wave_id - NMW : wave_id;  // index within its role
   const int wm = wave % WM;
   const int wn = wave / WM;
 
@@ -159,6 +171,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(ConvArgs a) {
     for (int j = 0; j < CPW; ++j) copy(t, stage, j);
   };
 
+  if (NCW > 0 && copier) {
+    // copy wave: keep two stages in flight ahead of the MFMA waves
+    issue(s_begin);
+    if (s_begin + 1 < s_end) issue(s_begin + 1);
+    for (int st = s_begin; st < s_end; ++st) {
+      if (st + 1 < s_end)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPW) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // stage st is visible to the MFMA waves, and they are done with stage
+      // st - 1, whose buffer stage st + 2 overwrites
+      __syncthreads();
+      if (st + 2 < s_end) issue(st + 2);
+    }
+    return;
+  }
+
   // Fragment read offsets inside a stage buffer, per k-step half h.
   int aoff[2][FN], boff[2][FM];
 #pragma unroll
@@ -177,9 +206,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(ConvArgs a) {
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  issue(s_begin);
-  if (s_begin + 1 < s_end) issue(s_begin + 1);
-  for (int st = s_begin; st < s_end; ++st) {
+  if (NCW > 0) {
+    // MFMA wave of a split workgroup: the copy waves fill the ring
+    for (int st = s_begin; st < s_end; ++st) {
+      __syncthreads();
+      const int8_t *buf = smem + ((st - s_begin) % kRing) * kTile;
+      v4i af[2][FN], bf[2][FM];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i) af[h][i] = *reinterpret_cast<const v4i *>(buf + aoff[h][i]);
+#pragma unroll
+        for (int j = 0; j < FM; ++j) bf[h][j] = *reinterpret_cast<const v4i *>(buf + boff[h][j]);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j) acc[i][j] = mfma16(af[h][i], bf[h][j], acc[i][j]);
+    }
+  }
+  if (NCW == 0) issue(s_begin);
+  if (NCW == 0 && s_begin + 1 < s_end) issue(s_begin + 1);
+  for (int st = s_begin; NCW == 0 && st < s_end; ++st) {
     // stage st has landed once only stage st + 1 (if any) is outstanding
     if (st + 1 < s_end)
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPW) : "memory");
@@ -243,14 +293,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_dma_kernel(ConvArgs a) {
   }
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int NCW = 0>
 int launch_tile(const ConvArgs &a, int splits, hipStream_t stream) {
   const int tiles = int(((int64_t(a.gemm_m) + BM - 1) / BM) * ((a.gemm_n + BN - 1) / BN));
   const int stages = a.gemm_k / kStageBytes;
   const int ring = std::min(kRing, splits > 1 ? a.stages_per_split : stages);
   const size_t lds = size_t(ring) * size_t(BM + BN) * kStageBytes;
-  auto kern = splits > 1 ? gemm_dma_kernel<BM, BN, WM, WN, true>
-                         : gemm_dma_kernel<BM, BN, WM, WN, false>;
+  auto kern = splits > 1 ? gemm_dma_kernel<BM, BN, WM, WN, true, NCW>
+                         : gemm_dma_kernel<BM, BN, WM, WN, false, NCW>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
@@ -259,8 +309,8 @@ int launch_tile(const ConvArgs &a, int splits, hipStream_t stream) {
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(tiles), unsigned(splits)), dim3(64 * WM * WN), lds,
-                     stream, a);
+  hipLaunchKernelGGL(kern, dim3(unsigned(tiles), unsigned(splits)), dim3(64 * (WM * WN + NCW)),
+                     lds, stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error(std::string("pipelined gemm kernel launch: ") + hipGetErrorString(e));
@@ -280,6 +330,16 @@ bool gemm_dma_tile_supported(int bm, int bn) {
   }
 }
 
+int gemm_dma_copy_waves(const GemmPlan &p) {
+  // Copy waves pay off once a workgroup has a steady state to overlap: with
+  // two or three k-stages the MFMA waves mostly wait on the first copies
+  // anyway, and the split roles only add a barrier hop per stage.
+  // The planner picks 256 x 128 only for more than four k-stages.
+  const int per_workgroup = p.splits > 1 ? p.stages_per_split : p.stages;
+  if (p.bm == 256 && p.bn == 128) return 4;
+  return p.bm == 128 && p.bn == 128 && per_workgroup >= 4 ? 4 : 0;
+}
+
 int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   // the kernel's assumptions, checked on the host: whole 128-byte stages in
@@ -293,13 +353,16 @@ int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stre
     set_error("pipelined gemm plan out of range");
     return I8CONV_BAD_ARGUMENT;
   }
-  // eight waves, two per SIMD (wave tiles 64 x 64, or 64 x 32 on the
-  // narrower tiles), except the small 128 x 64 tile
+  // eight MFMA waves, two per SIMD (wave tiles 64 x 64, or 64 x 32 on the
+  // narrower tiles), except the small 128 x 64 tile; plus four copy waves on
+  // the wide tiles when the workgroup has k-stages enough
+  const bool spec = gemm_dma_copy_waves(p) > 0;
   switch (p.bm * 1000 + p.bn) {
     case 128064: return launch_tile<128, 64, 2, 2>(a, splits, s);
-    case 128128: return launch_tile<128, 128, 2, 4>(a, splits, s);
+    case 128128:
+      return spec ? launch_tile<128, 128, 2, 4, 4>(a, splits, s) : launch_tile<128, 128, 2, 4>(a, splits, s);
     case 256064: return launch_tile<256, 64, 4, 2>(a, splits, s);
-    case 256128: return launch_tile<256, 128, 4, 2>(a, splits, s);
+    case 256128: return launch_tile<256, 128, 4, 2, 4>(a, splits, s);
   }
   set_error("unsupported pipelined gemm tile");
   return I8CONV_BAD_ARGUMENT;

@@ -56,7 +56,8 @@ EDGE = {
     "dma_5x3_asym": lab.ConvShape(1, 40, 36, 128, 136, 5, 3, 2, 0, 1, 2, 1, 3),
     "dma_grid_9x2": lab.ConvShape(1, 48, 48, 128, 200, 3, 3, 1, 1, 1, 1, 1, 1),
     "dma_256x128_tails": lab.ConvShape(4, 63, 99, 128, 134, 3, 3, 1, 1, 1, 1, 1, 1),
-    "dma_256x64_tails": lab.ConvShape(16, 56, 55, 256, 62, 1, 1, 0, 0, 1, 1, 1, 1),
+    "dma_1x1_k62_short": lab.ConvShape(16, 56, 55, 256, 62, 1, 1, 0, 0, 1, 1, 1, 1),
+    "dma_256x64_tails": lab.ConvShape(16, 57, 55, 128, 62, 3, 3, 1, 1, 1, 1, 1, 1),
     # c == 128 3x3 stride 1: the two-pass row-streaming kernel.  Blocks of
     # unequal height (8/7 and 2/1 output rows), a channel tail with scalar
     # stores, four fragments per row, no padding.
