@@ -160,16 +160,54 @@ __device__ __forceinline__ v4i load_bias4(const int32_t *base, int count, int i0
   return v;
 }
 
-// Final-output stores.  16-byte stores are non-temporal: the int32 output of
-// a layer is several times larger than its int8 input and filter, and
-// written once, so it is streamed through the L2 with the evict-first
-// policy instead of pushing the input rows and filter (read by every
-// workgroup) out of it.  The 4-byte stores of a channel tail (N % 4 != 0)
-// stay ordinary: each covers a sliver of a line, and only ordinary stores
-// are merged into whole lines in the L2 (non-temporal ones went to HBM as
-// partial writes and made such layers several times slower).
-__device__ __forceinline__ void store_out4(int32_t *dst, v4i v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<v4i *>(dst));
+// Final-output stores.  The 16-byte stores go through a buffer resource
+// over the workgroup's output rows (out_window) with one of two cache
+// policies (the aux operand of the gfx950 buffer-store builtins), chosen per
+// kernel by measurement:
+//  * kStoreThrough, sc1 (bit 4): device-scope write-through.  For kernels
+//    whose stores are spread over their whole run (the row-streaming
+//    kernels) and for split-K partial sums: without it the lines stay dirty
+//    in the L2 and the release at the end of the kernel writes them back
+//    after the last wave has finished, which the next launch on the stream
+//    waits for (28x28x128 layer: 7.8 -> 7.1 us per launch; split-K on the
+//    deep-K layer 15.1 -> 14.6 us).
+//  * kStoreStream, nt (bit 1): evict-first lines written back by the L2.
+//    For the pipelined GEMM, which stores a whole tile in one burst at its
+//    end: the L2 absorbs the burst faster than memory would (stride-2 3x3
+//    layer: 15.5 us, 16.7 us with write-through).  The output of a layer is
+//    several times larger than its input and filter and is written once, so
+//    evict-first keeps the input rows and filter in the L2.
+// (sc1 and nt together made the K = 36 row-kernel layer 25 % slower.)
+// The 4-byte stores of a channel tail (N % 4 != 0) stay ordinary: each
+// covers a sliver of a line, and only ordinary stores are merged into whole
+// lines in the L2 (non-temporal ones went to HBM as partial writes and made
+// such layers several times slower).
+constexpr int kStoreThrough = 16;
+constexpr int kStoreStream = 2;
+
+template <int kPolicy>
+__device__ __forceinline__ void store_out4(__amdgpu_buffer_rsrc_t out, uint32_t byte_off, v4i v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, out, byte_off, 0, kPolicy);
+}
+
+// A workgroup's output window: a buffer resource over pixels (GEMM rows)
+// [m0, m0 + rows) of an [M][N] int32 tensor, clamped to M, so that
+// store_out4 offsets are byte offsets from pixel m0 and fit 32 bits even
+// where the whole output does not.  ok is false when the window itself is
+// 2 GiB or more (absurdly wide N): the caller then takes its element path.
+struct OutWindow {
+  __amdgpu_buffer_rsrc_t r;
+  bool ok;
+};
+
+__device__ __forceinline__ OutWindow out_window(int32_t *y, int64_t gemm_m, int n, int64_t m0,
+                                                int64_t rows) {
+  const int64_t rr = min(rows, gemm_m - m0);
+  const int64_t bytes = rr > 0 ? rr * int64_t(n) * 4 : 0;
+  OutWindow w;
+  w.ok = bytes < (int64_t(1) << 31);
+  w.r = make_rsrc(y + m0 * int64_t(n), w.ok ? uint32_t(bytes) : 0u);
+  return w;
 }
 __device__ __forceinline__ void store_out1(int32_t *dst, int32_t v) { *dst = v; }
 

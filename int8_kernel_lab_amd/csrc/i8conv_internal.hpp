@@ -90,6 +90,8 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream);
 // kernel_rowpass.hip: fragments per output row of its instance for out_w
 // (0: none), and its LDS bytes for wp padded columns and `rows` output rows
 int rowpass_nfr(int out_w);
+// ... and the most output rows per block it has an instance for
+int rowpass_max_rows(int nfr);
 size_t rowpass_lds_bytes(int wp, int rows);
 // Whether kernel_row.hip has an instance for 16*fn channels per wave, cg
 // 64-channel groups and nfr 16-column fragments per output row.

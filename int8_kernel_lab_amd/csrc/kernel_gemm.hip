@@ -169,7 +169,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(ConvArgs a) {
   // Epilogue: lane holds channels oc0..oc0+3 of pixel px for each fragment.
   int32_t *out = a.y;
   if (kSplit) out = a.partial + size_t(blockIdx.y) * size_t(a.gemm_m) * size_t(a.gemm_n);
-  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const OutWindow ow = out_window(out, a.gemm_m, a.gemm_n, tile_m, BM);
+  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ow.ok;
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
@@ -184,10 +185,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(ConvArgs a) {
       const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
       if (px >= a.gemm_m) continue;
       const v4i v = add_wrap(acc[i][j], bv);
-      int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
       if (vec) {
-        if (oc0 < a.gemm_n) *reinterpret_cast<v4i *>(dst) = v;
+        if (oc0 < a.gemm_n)
+          store_out4<kSplit ? kStoreThrough : kStoreStream>(ow.r, (uint32_t(px - tile_m) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
       } else {
+        int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (oc0 + e < a.gemm_n) dst[e] = v[e];
@@ -205,23 +207,29 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_vec(
   // channel group q mod n4 is found once and then advanced by G mod n4,
   // so the loop has no 64-bit division.  The splits are added eight loads
   // at a time (all in flight together), still in split order.
+  // The stores go through a window over the workgroup's kThreads items of
+  // the pass (base qb, uniform), so 16-byte offsets stay small.
   const size_t grid = size_t(gridDim.x) * kThreads;
   const int step4 = int(grid % size_t(n4));
-  size_t q = size_t(blockIdx.x) * kThreads + threadIdx.x;
-  int c4 = int(q % size_t(n4));
-  for (; q < total4; q += grid) {
-    const v4i *src = reinterpret_cast<const v4i *>(partial) + q;
-    v4i acc = reinterpret_cast<const v4i *>(bias)[c4];
-    int sp = 0;
-    for (; sp + 8 <= splits; sp += 8) {
-      v4i t[8];
+  int c4 = int((size_t(blockIdx.x) * kThreads + threadIdx.x) % size_t(n4));
+  for (size_t qb = size_t(blockIdx.x) * kThreads; qb < total4; qb += grid) {
+    const size_t q = qb + threadIdx.x;
+    if (q < total4) {
+      const v4i *src = reinterpret_cast<const v4i *>(partial) + q;
+      v4i acc = reinterpret_cast<const v4i *>(bias)[c4];
+      int sp = 0;
+      for (; sp + 8 <= splits; sp += 8) {
+        v4i t[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = src[size_t(sp + u) * total4];
+        for (int u = 0; u < 8; ++u) t[u] = src[size_t(sp + u) * total4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc = add_wrap(acc, t[u]);
+        for (int u = 0; u < 8; ++u) acc = add_wrap(acc, t[u]);
+      }
+      for (; sp < splits; ++sp) acc = add_wrap(acc, src[size_t(sp) * total4]);
+      const auto y_r = make_rsrc(reinterpret_cast<v4i *>(y) + qb,
+                                 uint32_t(min(size_t(kThreads), total4 - qb)) * 16u);
+      store_out4<kStoreThrough>(y_r, uint32_t(threadIdx.x) * 16u, acc);
     }
-    for (; sp < splits; ++sp) acc = add_wrap(acc, src[size_t(sp) * total4]);
-    reinterpret_cast<v4i *>(y)[q] = acc;
     c4 += step4;
     if (c4 >= n4) c4 -= n4;
   }

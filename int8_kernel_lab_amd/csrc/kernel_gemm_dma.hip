@@ -271,7 +271,8 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
   // Epilogue: lane holds channels oc0..oc0+3 of pixel px for each fragment.
   int32_t *out = a.y;
   if (kSplit) out = a.partial + size_t(blockIdx.y) * size_t(a.gemm_m) * size_t(a.gemm_n);
-  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  const OutWindow ow = out_window(out, a.gemm_m, a.gemm_n, tile_m, BM);
+  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ow.ok;
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
@@ -281,10 +282,11 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
       const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
       if (px >= a.gemm_m) continue;
       const v4i v = add_wrap(acc[i][j], bv);
-      int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
       if (vec) {
-        if (oc0 < a.gemm_n) store_out4(dst, v);
+        if (oc0 < a.gemm_n)
+          store_out4<kSplit ? kStoreThrough : kStoreStream>(ow.r, (uint32_t(px - tile_m) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
       } else {
+        int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (oc0 + e < a.gemm_n) store_out1(dst + e, v[e]);

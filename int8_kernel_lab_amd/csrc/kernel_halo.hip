@@ -150,7 +150,9 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
 #pragma unroll
   for (int i = 0; i < FN; ++i)
     bv[i] = *reinterpret_cast<const v4i *>(bias_lds + (i * 16 + 4 * (lane >> 4)) * 4);
-  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  // output window: the pass's NF fragments of 16 pixels from pixel 16*f0
+  const OutWindow ow = out_window(a.y, a.gemm_m, a.gemm_n, int64_t(f0) * 16, NF * 16);
+  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && ow.ok;
 #pragma unroll
   for (int j = 0; j < NF; ++j) {
     if (mpx[j] < 0) continue;
@@ -158,10 +160,11 @@ __device__ __forceinline__ void halo_pass(const ConvArgs &a, const HaloArgs &p,
     for (int i = 0; i < FN; ++i) {
       const int oc0 = tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4);
       const v4i v = add_wrap4(acc[j][i], bv[i]);
-      int32_t *dst = a.y + size_t(mpx[j]) * size_t(a.gemm_n) + oc0;
       if (vec) {
-        if (oc0 < a.gemm_n) store_out4(dst, v);
+        if (oc0 < a.gemm_n)
+          store_out4<kStoreStream>(ow.r, (uint32_t(mpx[j] - f0 * 16) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
       } else {
+        int32_t *dst = a.y + size_t(mpx[j]) * size_t(a.gemm_n) + oc0;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (oc0 + e < a.gemm_n) store_out1(dst + e, v[e]);

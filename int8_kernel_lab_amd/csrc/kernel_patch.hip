@@ -188,7 +188,10 @@ __global__ __launch_bounds__(kThreads) void patch_kernel(ConvArgs a, PatchArgs p
     __syncthreads();
   }
 
-  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  // output window: the tile's output rows oy0 .. oy0 + th - 1 of image img
+  const int64_t m_win = (int64_t(img) * a.out_h + oy0) * a.out_w;
+  const OutWindow ow = out_window(a.y, a.gemm_m, a.gemm_n, m_win, int64_t(p.th) * a.out_w);
+  const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 && ow.ok;
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int oc0 = tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4);
@@ -207,10 +210,11 @@ __global__ __launch_bounds__(kThreads) void patch_kernel(ConvArgs a, PatchArgs p
       if (oy >= a.out_h || ox >= a.out_w) continue;
       const size_t m = size_t((img * a.out_h + oy) * a.out_w + ox);
       const v4i v = add_wrap(acc[i][f], bv);
-      int32_t *dst = a.y + m * size_t(a.gemm_n) + oc0;
       if (vec) {
-        if (oc0 < a.gemm_n) *reinterpret_cast<v4i *>(dst) = v;
+        if (oc0 < a.gemm_n)
+          store_out4<kStoreStream>(ow.r, (uint32_t(int64_t(m) - m_win) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
       } else {
+        int32_t *dst = a.y + m * size_t(a.gemm_n) + oc0;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (oc0 + e < a.gemm_n) dst[e] = v[e];

@@ -143,8 +143,10 @@ __device__ __forceinline__ void row_step(const RowArgs &p, RowState<FN, CG, NFR>
 #pragma unroll
   for (int i = 0; i < FN; ++i)
     bv[i] = *reinterpret_cast<const v4i *>(bias_lds + (i * 16 + 4 * (lane >> 4)) * 4);
-  const bool vec = (p.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
   const int m_row = m_row0 + (ir - 2) * p.out_w;
+  // output window: this output row's out_w pixels
+  const OutWindow ow = out_window(p.y, int64_t(p.n) * p.out_h * p.out_w, p.gemm_n, m_row, p.out_w);
+  const bool vec = (p.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0 && ow.ok;
 #pragma unroll
   for (int j = 0; j < NFR; ++j) {
     const int col = 16 * j + (lane & 15);
@@ -153,10 +155,11 @@ __device__ __forceinline__ void row_step(const RowArgs &p, RowState<FN, CG, NFR>
     for (int i = 0; i < FN; ++i) {
       const int oc0 = tile_n + wave * 16 * FN + i * 16 + 4 * (lane >> 4);
       const v4i v = add_wrap4(st.acc[s2][j][i], bv[i]);
-      int32_t *dst = p.y + size_t(m_row + col) * size_t(p.gemm_n) + oc0;
       if (vec) {
-        if (oc0 < p.gemm_n) store_out4(dst, v);
+        if (oc0 < p.gemm_n)
+          store_out4<kStoreThrough>(ow.r, (uint32_t(col) * uint32_t(p.gemm_n) + uint32_t(oc0)) * 4u, v);
       } else {
+        int32_t *dst = p.y + size_t(m_row + col) * size_t(p.gemm_n) + oc0;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (oc0 + e < p.gemm_n) store_out1(dst + e, v[e]);

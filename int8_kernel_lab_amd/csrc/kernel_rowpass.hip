@@ -119,8 +119,9 @@ struct PassState {
   }
 
   // Output row O: the accumulators already hold bias + dot products.  N % 4
-  // == 0 (and a 16-byte aligned output): one 16-byte non-temporal buffer
-  // store per fragment, no address arithmetic; otherwise element stores.
+  // == 0 (and a 16-byte aligned output): one 16-byte buffer store per
+  // fragment (write-through, kStoreThrough) at a scalar row offset, no
+  // address arithmetic; otherwise element stores.
   template <int O>
   __device__ __forceinline__ void store_row(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                             int oc0, int lane) {
@@ -128,7 +129,8 @@ struct PassState {
     if (vec) {
 #pragma unroll
       for (int j = 0; j < NFR; ++j)
-        __builtin_amdgcn_raw_buffer_store_b128(acc[O][j], yr, voff[j], O * row_stride, 2 /* nt */);
+        __builtin_amdgcn_raw_buffer_store_b128(acc[O][j], yr, voff[j], O * row_stride,
+                                               kStoreThrough);
       return;
     }
     const int m_row = m_row0 + O * p.out_w;
@@ -150,15 +152,46 @@ struct PassState {
   }
 };
 
+// Cross-wave signals in LDS: a wave adds 1 to a counter once its copies
+// have landed (its own vmcnt says so: LDS-DMA data is in LDS when the count
+// drops), and a consumer polls the counter.  The wait is bounded: after
+// kSpinLimit polls (far beyond any real copy time) it gives up, so every
+// wave always reaches the end of the kernel.
+constexpr int kSpinLimit = 1 << 20;
+
+__device__ __forceinline__ void flag_add(uint32_t addr) {
+  asm volatile("ds_add_u32 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(addr), "v"(1) : "memory");
+}
+
+__device__ __forceinline__ void flag_wait(uint32_t addr, int target) {
+  for (int spin = 0; spin < kSpinLimit; ++spin) {
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+    if (__builtin_amdgcn_readfirstlane(v) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Eight waves: waves 0-3 run the MFMAs (16 output channels each), waves 4-7
+// only copy the group-1 half of the operands.  A wave that is issuing copies
+// stalls while the compute unit's memory pipeline is full (all 256 compute
+// units copy at once at kernel start), so the MFMA waves issue only the
+// group-0 copies and the copy waves issue the group-1 copies after them:
+// pass 0 starts as soon as group 0 has landed, while group 1 is still
+// arriving.  Signals: flag 0 counts MFMA waves whose group-0 copies have
+// landed, flag 1 copy waves whose group-1 copies have landed.
 template <int R, int NFR>
-__global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
+__global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
   const PassArgs p = p_arg;
   pin_sgprs(p);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool copier = wave_id >= 4;
+  // the MFMA wave this wave is (or copies the group-1 filter rows for)
+  const int wave = wave_id & 3;
 
   const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
   const int tn = int(blockIdx.x) - rest * p.tiles_n;
@@ -168,22 +201,23 @@ __global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
   const int rows_out = int((int64_t(q + 1) * p.out_h) / p.blocks) - oy0;  // <= R
   const int tile_n = tn * 64;
 
-  // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows][ring: 18 KB per wave]
+  // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows]
+  //      [ring: 18 KB per wave][flags]
   const int8_t *bias_lds = smem + wave * 256;
-  stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, bias_lds, lane);
   PassState<R, NFR> st;
   st.planes = smem + kHaloBiasLds;
   st.plane_bytes = p.plane_copies * 1024;
   const int8_t *ring = st.planes + kGroups * p.rows_in * st.plane_bytes;
+  const uint32_t flags = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
   const v4u xd = make_desc(p.x, p.x_bytes);
   const v4u wd = make_desc(p.w, p.w_bytes);
   const uint32_t planes_lds = lds_addr(st.planes);
 
-  // This wave's copies of the group-G plane of every input row: copy qq
-  // covers units [64j, 64j + 64) of row rr's plane; unit u of pixel pix is
-  // slot pix*5 + u (u == 4: padding, left out of range -> zeros).
+  // Copies of the group-G plane of every input row, every fourth one from
+  // copy number `wave`: copy qq covers units [64j, 64j + 64) of row rr's
+  // plane; unit u of pixel pix is slot pix*5 + u (u == 4: padding, left out
+  // of range -> zeros).
   const int plane_total = p.rows_in * p.plane_copies;
-  const int my_plane_copies = plane_total > wave ? (plane_total - wave + 3) / 4 : 0;
   auto copy_planes = [&](int g) {
     for (int qq = wave; qq < plane_total; qq += 4) {
       const int rr = int(fast_div(uint32_t(qq), p.div_plane_copies));
@@ -202,8 +236,9 @@ __global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
       lds_copy16(xd, planes_lds + uint32_t((g * p.rows_in + rr) * st.plane_bytes + j * 1024), off);
     }
   };
-  // This wave's filter halves of group G: lane -> filter row 16*wave + lane/4
-  // and 16-byte chunk lane%4, holding the chunk swz64 puts in that slot.
+  // Filter halves of group G for MFMA wave `wave`: lane -> filter row
+  // 16*wave + lane/4 and 16-byte chunk lane%4, holding the chunk swz64 puts
+  // in that slot.
   const int frow = lane >> 2;
   const int fchunk = swz64_chunk(frow, lane & 3);
   const int oc_copy = tile_n + wave * 16 + frow;
@@ -217,18 +252,31 @@ __global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
       lds_copy16(wd, ring_lds + uint32_t((g * kTaps + t) * 1024),
                  fbase + uint32_t(t * 128 + g * 64));
   };
+
+  if (copier) {
+    __syncthreads();  // the MFMA waves have issued the group-0 copies
+    copy_planes(1);
+    copy_filter(1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0) flag_add(flags + 4);
+    return;
+  }
+
+  if (wave == 0 && lane == 0) {
+    // both flags start at zero; published by the barrier below, before any add
+    asm volatile("ds_write_b64 %0, %1" ::"v"(flags), "v"(uint64_t(0)) : "memory");
+  }
+  stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, bias_lds, lane);
+  copy_planes(0);
+  copy_filter(0);
+  __syncthreads();
+
   auto take_filter = [&](int g) {
     const int8_t *src = ring + (wave * kHalves + g * kTaps) * 1024;
 #pragma unroll
     for (int t = 0; t < kTaps; ++t)
       st.wf[t] = *reinterpret_cast<const v4i *>(src + t * 1024 + swz64(lane & 15, lane >> 4));
   };
-
-  copy_planes(0);
-  copy_filter(0);
-  copy_planes(1);
-  copy_filter(1);
-
 #pragma unroll
   for (int fx = 0; fx < 3; ++fx)
 #pragma unroll
@@ -250,10 +298,11 @@ __global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
                      : kOutOfRange;
   }
 
-  // Pass 0 once the bias, the group-0 planes and filter halves have landed:
-  // only this wave's group-1 copies (issued after them) may be in flight.
-  wait_vmcnt(my_plane_copies + kTaps);
-  __syncthreads();
+  // Pass 0 once the bias and every wave's group-0 planes and filter halves
+  // have landed.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (lane == 0) flag_add(flags);
+  flag_wait(flags, 4);
   take_filter(0);
   st.load_row(st.planes);
   // the accumulators start at the bias (the oracle adds the bias first)
@@ -263,9 +312,9 @@ __global__ __launch_bounds__(kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
 #pragma unroll
     for (int j = 0; j < NFR; ++j) st.acc[r][j] = bv;
   st.template pass<0>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
-  // Pass 1: everything has landed (no store has been issued yet).
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  // Pass 1 once the copy waves' group-1 copies have landed (no store has
+  // been issued yet).
+  flag_wait(flags + 4, 4);
   take_filter(1);
   st.load_row(st.planes + p.rows_in * st.plane_bytes);
   st.template pass<1>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
@@ -284,7 +333,7 @@ int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(kThreads), lds, s, h);
+  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(2 * kThreads), lds, s, h);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error(std::string("two-pass row kernel launch: ") + hipGetErrorString(e));
@@ -295,17 +344,21 @@ int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
 
 }  // namespace
 
-// Instances: R = 1..8 output rows per block, NFR = 1, 2 or 4 fragments per
-// output row (out_w <= 16, 32, 64).
+// Instances: R = 1..8 output rows per block with NFR = 1 or 2 fragments per
+// output row (out_w <= 16, 32), R = 1..4 with NFR = 4 (out_w <= 64): an MFMA
+// wave has 256 VGPRs when the workgroup runs eight waves, and R x NFR
+// accumulators beyond 32 fragments would spill.
 int rowpass_nfr(int out_w) {
   const int f = (out_w + 15) / 16;
   return f <= 2 ? f : (f <= 4 ? 4 : 0);
 }
 
+int rowpass_max_rows(int nfr) { return nfr == 4 ? 4 : 8; }
+
 size_t rowpass_lds_bytes(int wp, int rows) {
   const size_t plane_copies = (size_t(wp) * kUnits + 63) / 64;
   return size_t(kHaloBiasLds) + size_t(kGroups) * size_t(rows + 2) * plane_copies * 1024 +
-         size_t(4) * kHalves * 1024;
+         size_t(4) * kHalves * 1024 + 16;
 }
 
 int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
@@ -314,7 +367,8 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
   const int wp = a.wd + 2 * a.pad_w;
   const size_t lds = rowpass_lds_bytes(wp, R);
   if (a.r != 3 || a.s != 3 || a.stride_h != 1 || a.stride_w != 1 || a.dil_h != 1 ||
-      a.dil_w != 1 || a.c != 64 * kGroups || R < 1 || R > 8 || nfr == 0 || p.bn != 64 ||
+      a.dil_w != 1 || a.c != 64 * kGroups || R < 1 || nfr == 0 || R > rowpass_max_rows(nfr) ||
+      p.bn != 64 ||
       lds > size_t(kLdsBudget) || p.ranges < 1 || wp != a.out_w + 2 ||
       int64_t(a.out_h) > int64_t(p.ranges) * R ||
       int64_t(a.gemm_m) * a.gemm_n * 4 > int64_t(INT32_MAX)) {
@@ -355,7 +409,7 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
   if (R == RR) {                                                           \
     if (nfr == 1) return launch_t<RR, 1>(h, grid, lds, s);                 \
     if (nfr == 2) return launch_t<RR, 2>(h, grid, lds, s);                 \
-    return launch_t<RR, 4>(h, grid, lds, s);                               \
+    if constexpr (RR <= 4) return launch_t<RR, 4>(h, grid, lds, s);        \
   }
   I8_PASS_CASE(1) I8_PASS_CASE(2) I8_PASS_CASE(3) I8_PASS_CASE(4)
   I8_PASS_CASE(5) I8_PASS_CASE(6) I8_PASS_CASE(7) I8_PASS_CASE(8)
