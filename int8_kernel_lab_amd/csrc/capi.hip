@@ -101,11 +101,11 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
       const size_t row_bytes =
           size_t(halo_row_layout(shape->w + 2 * shape->pad_w, shape->c).row_bytes);
       const std::string lds =
-          p.pass2 ? std::to_string(rowpass_lds_bytes(shape->w + 2 * shape->pad_w, p.rows - 2) / 1024) +
+          p.streamed ? std::to_string(rowpass_lds_bytes(shape->w + 2 * shape->pad_w, p.rows - 2) / 1024) +
                         " KB"
                   : std::to_string((kHaloBiasLds + size_t(p.rows) * row_bytes) / 1024) + "+" +
                         std::to_string(p.ring * halo_ring_slot_bytes(p.bn / 64) / 1024) + " KB";
-      d = std::string(kNames[id]) + (p.pass2 ? " two-pass row-streaming: " : " row-streaming: ") +
+      d = std::string(kNames[id]) + (p.streamed ? " row-streaming with copy waves: " : " row-streaming: ") +
           std::to_string(p.ranges) + " row blocks/image of <=" + std::to_string(p.rows - 2) +
           " rows x " + std::to_string(p.bn) + "oc, " + std::to_string(p.frags_m) +
           " frags/row, LDS " + lds + ", grid " +
@@ -178,7 +178,7 @@ int i8conv_launch(int id, const i8conv_shape *shape, const int8_t *input,
         set_error(std::string(kNames[id]) + " is not eligible for this shape");
         return I8CONV_INELIGIBLE;
       }
-      return pp.row ? (pp.pass2 ? launch_rowpass(args, pp, stream) : launch_row(args, pp, stream))
+      return pp.row ? (pp.streamed ? launch_rowpass(args, pp, stream) : launch_row(args, pp, stream))
              : pp.resident ? launch_halo_resident(args, pp, stream)
                            : launch_patch(args, pp, stream);
     }

@@ -61,8 +61,8 @@ struct PatchPlan {
   // halo, 3x3 stride 1: output-row blocks streamed row by row with the
   // taps formed in registers (kernel_row.hip); `ranges` = blocks per image
   bool row = false;
-  // row-streaming, 128 channels: the two-pass form (kernel_rowpass.hip)
-  bool pass2 = false;
+  // row-streaming, 128 channels: the form with copy waves (kernel_rowpass.hip)
+  bool streamed = false;
   int ranges = 0;  // resident: pixel ranges per channel slice
   int rows = 0;    // resident: most padded input rows any range needs
   int ring = 0;    // resident: filter staging slots in LDS

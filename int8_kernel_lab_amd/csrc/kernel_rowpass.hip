@@ -1,30 +1,35 @@
-// Two-pass row-streaming 3x3 kernel for 128-channel layers on gfx950 INT8
-// MFMA: the row-streaming halo kernel (kernel_row.hip) reorganised so that
-// its MFMAs start after half of the workgroup's copies instead of all of
-// them.
+// Row-streaming 3x3 kernel for 128-channel layers on gfx950 INT8 MFMA,
+// with copy-only waves that stream the operands to the MFMA waves row by
+// row (the headline kernel of the 28x28x128 layer).
 //
-// Why.  A row-streaming workgroup copies its padded input rows and its
-// filter slice (16 output channels x 9 x 128 bytes per wave) into LDS
-// before most of its MFMAs can run: from the second input row on, every
-// row needs all nine taps.  At kernel start the L2s are cold and all 256
-// compute units copy at once, so that copy (about 120 KB per workgroup on
-// a 28x28x128 layer) is the longest single phase of the kernel.
+// Why.  A row-streaming workgroup (kernel_row.hip) copies its padded input
+// rows and its filter slice (16 output channels x 9 x 128 bytes per MFMA
+// wave) into LDS before most of its MFMAs can run.  At kernel start the L2s
+// are cold and all 256 compute units copy at once; one compute unit's
+// copies land at about 65 GB/s whatever the access pattern or wave count,
+// so the ~108 KB of a 28x28x128 workgroup take ~1.7 us, and a wave that
+// issues copies stalls while the memory pipeline is full.
 //
-// How.  Both operands are split by 64-channel group (cg = 0, 1) and copied
-// group by group: first the group-0 half of every input row and of the
-// filter, then the group-1 halves.  Pass 0 walks the input rows with the
-// group-0 data only and accumulates every output row of the block in
-// registers (R rows x NFR fragments); pass 1 repeats the walk with group 1
-// and completes output row ir - 2 at input row ir, which is stored one
-// input row later.
-// Pass 0 needs half of the bytes, and the group-1 copies land while it runs.
+// How.  Eight waves: four MFMA waves (16 output channels each) and four
+// copy waves.  The copy waves issue the copies in the order the MFMA waves
+// consume them, in chunks: padded input row r (both 64-channel groups),
+// preceded for r <= 2 by the taps of filter row r (input row r feeds output
+// rows r - fy, so filter row r is first needed at input row r), the bias
+// first of all.  Each copy wave signals a chunk through an LDS counter once
+// its copies of it have landed; the MFMA waves walk the input rows, wait for
+// each row's chunk just before reading it, and store output row o once it
+// is complete (one row after input row o + 2).  The MFMAs start after the
+// first chunk (~9 KB) instead of all the copies, and the stores are spread
+// over the walk.  With 4 fragments per row the registers do not hold both
+// groups: the walk then runs twice, group 0 (accumulating every output row
+// of the block) and group 1 (completing and storing them).
 //
 // Layouts.  Input: one LDS plane per (group, padded row): wp pixels x 80
 // bytes (the group's 64 channels, then 16 bytes of padding), so the 16
 // pixels of a fragment hit 16 distinct 16-byte bank groups (pitch 5 units).
-// Filter: per wave, 18 1 KB halves (group-major, then tap): 16 output
+// Filter: per MFMA wave, 18 1 KB halves (group-major, then tap): 16 output
 // channels x 64 bytes in the swz64 layout, copied with the swizzle applied
-// at the source.  Each wave copies and reads only its own filter rows.
+// at the source.
 //
 // Reuse and MFMAs are as in kernel_row.hip: the fragment of input row ir at
 // column offset fx feeds output rows ir - fy for fy = 0, 1, 2.
@@ -42,6 +47,10 @@ constexpr int kGroups = 2;      // 64-channel groups: c == 128
 constexpr int kUnits = 5;       // 16-byte units per pixel in a plane (4 data + 1 pad)
 constexpr int kTaps = 9;
 constexpr int kHalves = kTaps * kGroups;  // 1 KB filter halves per wave
+// Channel groups per row walk: 2 (one pass over the rows, both groups per
+// row) where the registers allow it, 1 (two passes, group 0 then group 1)
+// for 4 fragments per row, whose single-pass form would spill.
+constexpr int walk_groups(int nfr) { return nfr == 4 ? 1 : 2; }
 
 // Everything the kernel reads; loaded into SGPRs in one batch.
 struct PassArgs {
@@ -60,14 +69,50 @@ struct PassArgs {
   FastDiv3 div_plane_copies, div_hp, div_blocks, div_tiles_n;
 };
 
-template <int R, int NFR>
+// Cross-wave signals in LDS: a copy wave adds 1 to a chunk's counter once
+// its copies of that chunk have landed (its own vmcnt says so: LDS-DMA data
+// is in LDS when the count drops), and the MFMA waves poll the counter.
+// The wait is bounded: after kSpinLimit polls (far beyond any real copy
+// time) it gives up, so every wave always reaches the end of the kernel.
+constexpr int kSpinLimit = 1 << 20;
+constexpr int kCopyWaves = 4;
+
+// Adds 1 to the counter at LDS address addr (no wait: the wave waits for
+// its LDS operations once, before it ends).
+__device__ __forceinline__ void flag_add(uint32_t addr) {
+  asm volatile("ds_add_u32 %0, %1" ::"v"(addr), "v"(1) : "memory");
+}
+
+// A compiler-visible read of the counter at LDS address addr, issued ahead
+// of its use (the compiler waits for it where the value is needed).
+__device__ __forceinline__ int flag_peek(uint32_t addr) {
+  return *reinterpret_cast<volatile __attribute__((address_space(3))) int *>(size_t(addr));
+}
+
+__device__ __forceinline__ void flag_wait(uint32_t addr, int target) {
+  for (int spin = 0; spin < kSpinLimit; ++spin) {
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+    if (__builtin_amdgcn_readfirstlane(v) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Per-MFMA-wave state of a row walk over NG channel groups at a time: NG ==
+// 1 walks the rows twice (group 0, then group 1; the two-pass form), NG == 2
+// once with both groups per row (the single-pass form).
+template <int R, int NFR, int NG>
 struct PassState {
-  v4i wf[kTaps];           // this wave's 16 channels, one group, all taps (t = fy*3 + fx)
+  v4i wf[NG][kTaps];       // this wave's 16 channels, the walk's groups, all taps (t = fy*3 + fx)
   v4i acc[R][NFR];         // output rows of the block
-  v4i frag[3][NFR];        // fragments of the next input row (column offsets 0, 1, 2)
+  v4i frag[NG][3][NFR];    // fragments of the next input row (column offsets 0, 1, 2)
   int colofs[3][NFR];      // LDS offset of this lane's column + fx / k-block in a plane
   const int8_t *planes;    // group-0 planes, then group-1 planes
+  const int8_t *halves;    // this wave's filter halves: (group, tap) 1 KB each
+  const int8_t *bias_lds;  // this wave's 16 bias values
   int plane_bytes;
+  uint32_t counters;       // LDS address of the chunk counters
+  int peeked;              // counter of the next row's chunk, read one row ahead
   // Output, vector path: a buffer resource over y, this lane's byte offset
   // of output row 0 per fragment (out of range where the column or the
   // channels fall outside the layer: the store is dropped, no branch), and
@@ -76,37 +121,73 @@ struct PassState {
   uint32_t voff[NFR];
   uint32_t row_stride;
 
-  __device__ __forceinline__ void load_row(const int8_t *plane) {
+  template <int G>
+  __device__ __forceinline__ void load_row(const PassArgs &p, int r) {
 #pragma unroll
-    for (int fx = 0; fx < 3; ++fx)
+    for (int g = 0; g < NG; ++g) {
+      const int8_t *plane = planes + ((G + g) * p.rows_in + r) * plane_bytes;
 #pragma unroll
-      for (int j = 0; j < NFR; ++j)
-        frag[fx][j] = *reinterpret_cast<const v4i *>(plane + colofs[fx][j]);
+      for (int fx = 0; fx < 3; ++fx)
+#pragma unroll
+        for (int j = 0; j < NFR; ++j)
+          frag[g][fx][j] = *reinterpret_cast<const v4i *>(plane + colofs[fx][j]);
+    }
   }
 
-  // Input row IR of group G: MFMAs into output rows IR - fy (compile-time
-  // valid ones); in pass 1, output row IR - 2 is then complete and stored.
+  // Chunk of (first group G, padded input row r): chunks are numbered in the
+  // order the copy waves issue them (group-major when NG == 1).
+  template <int G>
+  __device__ __forceinline__ uint32_t counter(const PassArgs &p, int r) const {
+    return counters + 4u * uint32_t((G / NG) * p.rows_in + r);
+  }
+
+  template <int G, int FY>
+  __device__ __forceinline__ void take_taps(int lane) {
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int fx = 0; fx < 3; ++fx)
+        wf[g][FY * 3 + fx] = *reinterpret_cast<const v4i *>(
+            halves + ((G + g) * kTaps + FY * 3 + fx) * 1024 + swz64(lane & 15, lane >> 4));
+  }
+
+  // Input row IR of the walk from group G: once the next row's chunk has
+  // landed, its fragments (and the next filter row's taps) are read; then
+  // the MFMAs of this row into output rows IR - fy (compile-time valid
+  // ones); in the last walk, output row IR - 3 is then stored.  The counter
+  // of the chunk after next is read here and checked one row later, so a
+  // chunk that has landed costs no wait.
   template <int G, int IR>
   __device__ __forceinline__ void step(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                        int oc0, int lane) {
-    v4i cur[3][NFR];
+    v4i cur[NG][3][NFR];
 #pragma unroll
-    for (int fx = 0; fx < 3; ++fx)
+    for (int g = 0; g < NG; ++g)
 #pragma unroll
-      for (int j = 0; j < NFR; ++j) cur[fx][j] = frag[fx][j];
+      for (int fx = 0; fx < 3; ++fx)
+#pragma unroll
+        for (int j = 0; j < NFR; ++j) cur[g][fx][j] = frag[g][fx][j];
     if (IR + 1 < R + 2) {
-      load_row(planes + (G * p.rows_in + IR + 1) * plane_bytes);
+      const int seen = peeked;
+      if (IR + 2 < R + 2) peeked = flag_peek(counter<G>(p, IR + 2));
+      if (seen < kCopyWaves) flag_wait(counter<G>(p, IR + 1), kCopyWaves);
+      if (IR + 1 <= 2) take_taps<G, (IR + 1 <= 2 ? IR + 1 : 0)>(lane);
+      load_row<G>(p, IR + 1);
       // keep the reads here: the scheduler would otherwise sink them to their use
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int fx = 0; fx < 3; ++fx) {
+    for (int g = 0; g < NG; ++g) {
 #pragma unroll
-      for (int fy = 0; fy < 3; ++fy) {
-        const int o = IR - fy;  // a constant once the loops are unrolled
-        if (o >= 0 && o < R) {
+      for (int fx = 0; fx < 3; ++fx) {
 #pragma unroll
-          for (int j = 0; j < NFR; ++j) acc[o][j] = mfma16(wf[fy * 3 + fx], cur[fx][j], acc[o][j]);
+        for (int fy = 0; fy < 3; ++fy) {
+          const int o = IR - fy;  // a constant once the loops are unrolled
+          if (o >= 0 && o < R) {
+#pragma unroll
+            for (int j = 0; j < NFR; ++j)
+              acc[o][j] = mfma16(wf[g][fy * 3 + fx], cur[g][fx][j], acc[o][j]);
+          }
         }
       }
     }
@@ -114,7 +195,7 @@ struct PassState {
     // row later, so that its accumulators are read long after the MFMAs that
     // wrote them (reading them right away would stall the wave until those
     // MFMAs drained, every row).
-    if (G == kGroups - 1 && IR >= 3)
+    if (G + NG == kGroups && IR >= 3)
       store_row<(IR >= 3 ? IR - 3 : 0)>(p, vec, rows_out, m_row0, oc0, lane);
   }
 
@@ -145,42 +226,94 @@ struct PassState {
     }
   }
 
+  // The walk from group G over all R + 2 padded input rows.
   template <int G, size_t... I>
-  __device__ __forceinline__ void pass(const PassArgs &p, bool vec, int rows_out, int m_row0,
+  __device__ __forceinline__ void walk(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                        int oc0, int lane, std::index_sequence<I...>) {
+    flag_wait(counter<G>(p, 0), kCopyWaves);
+    peeked = flag_peek(counter<G>(p, 1));
+    take_taps<G, 0>(lane);
+    load_row<G>(p, 0);
+    if (G == 0) {
+      // the accumulators start at the bias (the oracle adds the bias first)
+      const v4i bv = *reinterpret_cast<const v4i *>(bias_lds + 16 * (lane >> 4));
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < NFR; ++j) acc[r][j] = bv;
+    }
     (step<G, int(I)>(p, vec, rows_out, m_row0, oc0, lane), ...);
   }
 };
 
-// Cross-wave signals in LDS: a wave adds 1 to a counter once its copies
-// have landed (its own vmcnt says so: LDS-DMA data is in LDS when the count
-// drops), and a consumer polls the counter.  The wait is bounded: after
-// kSpinLimit polls (far beyond any real copy time) it gives up, so every
-// wave always reaches the end of the kernel.
-constexpr int kSpinLimit = 1 << 20;
-
-__device__ __forceinline__ void flag_add(uint32_t addr) {
-  asm volatile("ds_add_u32 %0, %1\n\ts_waitcnt lgkmcnt(0)" ::"v"(addr), "v"(1) : "memory");
-}
-
-__device__ __forceinline__ void flag_wait(uint32_t addr, int target) {
-  for (int spin = 0; spin < kSpinLimit; ++spin) {
-    int v;
-    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
-    if (__builtin_amdgcn_readfirstlane(v) >= target) return;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
 // Eight waves: waves 0-3 run the MFMAs (16 output channels each), waves 4-7
-// only copy the group-1 half of the operands.  A wave that is issuing copies
-// stalls while the compute unit's memory pipeline is full (all 256 compute
-// units copy at once at kernel start), so the MFMA waves issue only the
-// group-0 copies and the copy waves issue the group-1 copies after them:
-// pass 0 starts as soon as group 0 has landed, while group 1 is still
-// arriving.  Signals: flag 0 counts MFMA waves whose group-0 copies have
-// landed, flag 1 copy waves whose group-1 copies have landed.
-template <int R, int NFR>
+// only copy.  The copies are issued in chunks, in the order the MFMA waves
+// consume them: padded input row r (of the walk's groups), preceded for
+// r <= 2 by the filter taps of filter row r (the first row an input row
+// needs them at: input row r feeds output rows r - fy), and the bias first
+// of all.  Copy wave w copies MFMA wave w's filter halves and plane copies
+// j = w + 4i of every row.  A copy wave signals chunk c (adds 1 to its
+// counter) once its copies of c have landed, and the MFMA waves wait for
+// each row's chunk just before reading it: the MFMAs start after the first
+// chunk instead of half or all of the copies.
+constexpr int kSignalLag = 4;
+
+// The copy waves' schedule, unrolled at compile time (R + 2 padded input
+// rows per walk, NG groups per chunk, PW plane copies per row and group
+// from this wave): chunk k is issued in order, and chunk c is signalled
+// right after issuing the first chunk k that puts kSignalLag or more of this
+// wave's copies after c (vmcnt(after) then covers c), or after vmcnt(0) at
+// the end.  Straight-line code: a copy wave's scalar work per chunk is a
+// few instructions, so its issue keeps up with the copies (a loop with a
+// run-time vmcnt switch per chunk was several times slower).
+template <int R, int PW, int NG>
+struct CopySchedule {
+  static constexpr int kRows = R + 2;
+  static constexpr int kChunks = (kGroups / NG) * kRows;
+  static constexpr int copies(int k) {
+    return (k == 0 ? 1 : 0) + (k % kRows <= 2 ? 3 * NG : 0) + NG * PW;
+  }
+  static constexpr int after(int c, int k) {
+    int n = 0;
+    for (int i = c + 1; i <= k; ++i) n += copies(i);
+    return n;
+  }
+  static constexpr int signal_at(int c) {
+    for (int k = c; k < kChunks; ++k)
+      if (after(c, k) >= kSignalLag) return k;
+    return kChunks;
+  }
+
+  template <int K, int C, class Signal>
+  __device__ static __forceinline__ void maybe_signal(Signal &signal) {
+    if constexpr (signal_at(C) == K) {
+      if constexpr (K < kChunks) {
+        constexpr int n = after(C, K) < 63 ? after(C, K) : 63;
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+      }
+      signal(C);
+    }
+  }
+  template <int K, class Signal, size_t... C>
+  __device__ static __forceinline__ void signals(Signal &signal, std::index_sequence<C...>) {
+    (maybe_signal<K, int(C)>(signal), ...);
+  }
+  template <class Issue, class Signal, size_t... K>
+  __device__ static __forceinline__ void steps(Issue &issue, Signal &signal,
+                                               std::index_sequence<K...>) {
+    ((issue((int(K) / kRows) * NG, int(K) % kRows, PW, NG),
+      signals<int(K)>(signal, std::make_index_sequence<kChunks>{})),
+     ...);
+  }
+  template <class Issue, class Signal>
+  __device__ static __forceinline__ void run(Issue &issue, Signal &signal) {
+    steps(issue, signal, std::make_index_sequence<kChunks>{});
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    signals<kChunks>(signal, std::make_index_sequence<kChunks>{});
+  }
+};
+
+template <int R, int NFR, int NG>
 __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
   const PassArgs p = p_arg;
@@ -190,7 +323,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   const int lane = tid & 63;
   const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool copier = wave_id >= 4;
-  // the MFMA wave this wave is (or copies the group-1 filter rows for)
+  // the MFMA wave this wave is (or copies the filter halves and bias for)
   const int wave = wave_id & 3;
 
   const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
@@ -202,81 +335,84 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   const int tile_n = tn * 64;
 
   // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows]
-  //      [ring: 18 KB per wave][flags]
-  const int8_t *bias_lds = smem + wave * 256;
-  PassState<R, NFR> st;
+  //      [filter halves: 18 KB per wave][chunk counters]
+  PassState<R, NFR, NG> st;
+  st.bias_lds = smem + wave * 256;
   st.planes = smem + kHaloBiasLds;
   st.plane_bytes = p.plane_copies * 1024;
   const int8_t *ring = st.planes + kGroups * p.rows_in * st.plane_bytes;
-  const uint32_t flags = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
-  const v4u xd = make_desc(p.x, p.x_bytes);
-  const v4u wd = make_desc(p.w, p.w_bytes);
-  const uint32_t planes_lds = lds_addr(st.planes);
+  st.halves = ring + wave * kHalves * 1024;
+  st.counters = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
+  const int nchunks = (kGroups / NG) * p.rows_in;
 
-  // Copies of the group-G plane of every input row, every fourth one from
-  // copy number `wave`: copy qq covers units [64j, 64j + 64) of row rr's
-  // plane; unit u of pixel pix is slot pix*5 + u (u == 4: padding, left out
-  // of range -> zeros).
-  const int plane_total = p.rows_in * p.plane_copies;
-  auto copy_planes = [&](int g) {
-    for (int qq = wave; qq < plane_total; qq += 4) {
-      const int rr = int(fast_div(uint32_t(qq), p.div_plane_copies));
-      const int j = qq - rr * p.plane_copies;
-      const int vr = b * p.hp + oy0 + rr;
+  if (wave_id == 0 && lane < nchunks) {
+    // every counter starts at zero before any wave adds to it
+    asm volatile("ds_write_b32 %0, %1" ::"v"(st.counters + 4u * uint32_t(lane)), "v"(0)
+                 : "memory");
+  }
+  __syncthreads();
+
+  if (copier) {
+    const v4u xd = make_desc(p.x, p.x_bytes);
+    const v4u wd = make_desc(p.w, p.w_bytes);
+    const uint32_t planes_lds = lds_addr(st.planes);
+    // filter halves for MFMA wave `wave`: lane -> filter row 16*wave +
+    // lane/4 and 16-byte chunk lane%4, holding the chunk swz64 puts there
+    const int frow = lane >> 2;
+    const int fchunk = swz64_chunk(frow, lane & 3);
+    const int oc_copy = tile_n + wave * 16 + frow;
+    const uint32_t fbase = oc_copy < p.gemm_n
+                               ? uint32_t(oc_copy) * uint32_t(p.gemm_k) + uint32_t(16 * fchunk)
+                               : kOutOfRange;
+    const uint32_t halves_lds = lds_addr(st.halves);
+    // Chunk (groups g0 .. g0 + ng - 1, row r): the bias (first chunk), the
+    // filter taps of filter row r (r <= 2) and plane copies j = wave + 4i
+    // of padded input row r.  Copy j covers units [64j, 64j + 64) of the
+    // plane; unit u of pixel pix is slot pix*5 + u (u == 4: padding, left
+    // out of range -> zeros).
+    auto issue_chunk = [&](int g0, int r, int pw, int ng) {
+      if (g0 == 0 && r == 0) stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, st.bias_lds, lane);
+      for (int g = g0; g < g0 + ng; ++g) {
+        if (r <= 2) {
+#pragma unroll
+          for (int fx = 0; fx < 3; ++fx) {
+            const int t = 3 * r + fx;
+            lds_copy16(wd, halves_lds + uint32_t((g * kTaps + t) * 1024),
+                       fbase + uint32_t(t * 128 + g * 64));
+          }
+        }
+      }
+      const int vr = b * p.hp + oy0 + r;
       const int bb = int(fast_div(uint32_t(vr), p.div_hp));
       const int iy = vr - bb * p.hp - p.pad_h;
       const bool row_ok = bb < p.n && unsigned(iy) < unsigned(p.h);
-      // modulo 2^32: exact wherever it is used (the sum below is in [0, 2^31))
-      const uint32_t row_off = uint32_t((bb * p.h + iy) * p.wd - p.pad_w) * uint32_t(p.c) + uint32_t(64 * g);
-      const int slot = j * 64 + lane;
-      const int pix = slot / kUnits;
-      const int u = slot - pix * kUnits;
-      const bool ok = row_ok && u < kUnits - 1 && unsigned(pix - p.pad_w) < unsigned(p.wd);
-      const uint32_t off = ok ? row_off + uint32_t(pix * p.c + 16 * u) : kOutOfRange;
-      lds_copy16(xd, planes_lds + uint32_t((g * p.rows_in + rr) * st.plane_bytes + j * 1024), off);
-    }
-  };
-  // Filter halves of group G for MFMA wave `wave`: lane -> filter row
-  // 16*wave + lane/4 and 16-byte chunk lane%4, holding the chunk swz64 puts
-  // in that slot.
-  const int frow = lane >> 2;
-  const int fchunk = swz64_chunk(frow, lane & 3);
-  const int oc_copy = tile_n + wave * 16 + frow;
-  const uint32_t fbase = oc_copy < p.gemm_n
-                             ? uint32_t(oc_copy) * uint32_t(p.gemm_k) + uint32_t(16 * fchunk)
-                             : kOutOfRange;
-  const uint32_t ring_lds = lds_addr(ring) + uint32_t(wave * kHalves * 1024);
-  auto copy_filter = [&](int g) {
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t)
-      lds_copy16(wd, ring_lds + uint32_t((g * kTaps + t) * 1024),
-                 fbase + uint32_t(t * 128 + g * 64));
-  };
-
-  if (copier) {
-    __syncthreads();  // the MFMA waves have issued the group-0 copies
-    copy_planes(1);
-    copy_filter(1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (lane == 0) flag_add(flags + 4);
+      // modulo 2^32: exact wherever it is used (the sums below are in [0, 2^31))
+      const uint32_t row_off = uint32_t((bb * p.h + iy) * p.wd - p.pad_w) * uint32_t(p.c);
+      for (int g = g0; g < g0 + ng; ++g) {
+        for (int i = 0; i < pw; ++i) {
+          const int j = wave + 4 * i;
+          const int slot = j * 64 + lane;
+          const int pix = slot / kUnits;
+          const int u = slot - pix * kUnits;
+          const bool ok = row_ok && u < kUnits - 1 && unsigned(pix - p.pad_w) < unsigned(p.wd);
+          const uint32_t off = ok ? row_off + uint32_t(64 * g + pix * p.c + 16 * u) : kOutOfRange;
+          lds_copy16(xd, planes_lds + uint32_t((g * p.rows_in + r) * st.plane_bytes + j * 1024),
+                     off);
+        }
+      }
+    };
+    auto signal = [&](int c) {
+      if (lane == 0) flag_add(st.counters + 4u * uint32_t(c));
+    };
+    // plane copies per row and group this wave issues: j = wave, wave + 4
+    const int pw = p.plane_copies > wave ? (p.plane_copies - wave + 3) / 4 : 0;
+    if (pw == 0) CopySchedule<R, 0, NG>::run(issue_chunk, signal);
+    else if (pw == 1) CopySchedule<R, 1, NG>::run(issue_chunk, signal);
+    else CopySchedule<R, 2, NG>::run(issue_chunk, signal);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     return;
   }
 
-  if (wave == 0 && lane == 0) {
-    // both flags start at zero; published by the barrier below, before any add
-    asm volatile("ds_write_b64 %0, %1" ::"v"(flags), "v"(uint64_t(0)) : "memory");
-  }
-  stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, bias_lds, lane);
-  copy_planes(0);
-  copy_filter(0);
-  __syncthreads();
-
-  auto take_filter = [&](int g) {
-    const int8_t *src = ring + (wave * kHalves + g * kTaps) * 1024;
-#pragma unroll
-    for (int t = 0; t < kTaps; ++t)
-      st.wf[t] = *reinterpret_cast<const v4i *>(src + t * 1024 + swz64(lane & 15, lane >> 4));
-  };
 #pragma unroll
   for (int fx = 0; fx < 3; ++fx)
 #pragma unroll
@@ -298,32 +434,15 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
                      : kOutOfRange;
   }
 
-  // Pass 0 once the bias and every wave's group-0 planes and filter halves
-  // have landed.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (lane == 0) flag_add(flags);
-  flag_wait(flags, 4);
-  take_filter(0);
-  st.load_row(st.planes);
-  // the accumulators start at the bias (the oracle adds the bias first)
-  const v4i bv = *reinterpret_cast<const v4i *>(bias_lds + 16 * (lane >> 4));
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int j = 0; j < NFR; ++j) st.acc[r][j] = bv;
-  st.template pass<0>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
-  // Pass 1 once the copy waves' group-1 copies have landed (no store has
-  // been issued yet).
-  flag_wait(flags + 4, 4);
-  take_filter(1);
-  st.load_row(st.planes + p.rows_in * st.plane_bytes);
-  st.template pass<1>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
+  st.template walk<0>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
+  if constexpr (NG == 1)
+    st.template walk<1>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
   st.template store_row<R - 1>(p, vec, rows_out, m_row0, oc0, lane);
 }
 
 template <int R, int NFR>
 int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
-  auto kern = rowpass_kernel<R, NFR>;
+  auto kern = rowpass_kernel<R, NFR, walk_groups(NFR)>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -336,7 +455,7 @@ int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
   hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(2 * kThreads), lds, s, h);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
-    set_error(std::string("two-pass row kernel launch: ") + hipGetErrorString(e));
+    set_error(std::string("row kernel with copy waves, launch: ") + hipGetErrorString(e));
     return I8CONV_HIP_ERROR;
   }
   return I8CONV_OK;
@@ -358,7 +477,7 @@ int rowpass_max_rows(int nfr) { return nfr == 4 ? 4 : 8; }
 size_t rowpass_lds_bytes(int wp, int rows) {
   const size_t plane_copies = (size_t(wp) * kUnits + 63) / 64;
   return size_t(kHaloBiasLds) + size_t(kGroups) * size_t(rows + 2) * plane_copies * 1024 +
-         size_t(4) * kHalves * 1024 + 16;
+         size_t(4) * kHalves * 1024 + 128;  // + chunk counters (2 x up to 10 rows)
 }
 
 int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
@@ -370,9 +489,10 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
       a.dil_w != 1 || a.c != 64 * kGroups || R < 1 || nfr == 0 || R > rowpass_max_rows(nfr) ||
       p.bn != 64 ||
       lds > size_t(kLdsBudget) || p.ranges < 1 || wp != a.out_w + 2 ||
+      (wp * kUnits + 63) / 64 > 8 ||
       int64_t(a.out_h) > int64_t(p.ranges) * R ||
       int64_t(a.gemm_m) * a.gemm_n * 4 > int64_t(INT32_MAX)) {
-    set_error("two-pass row plan out of range");
+    set_error("row plan (copy waves) out of range");
     return I8CONV_BAD_ARGUMENT;
   }
   PassArgs h{};
@@ -414,7 +534,7 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
   I8_PASS_CASE(1) I8_PASS_CASE(2) I8_PASS_CASE(3) I8_PASS_CASE(4)
   I8_PASS_CASE(5) I8_PASS_CASE(6) I8_PASS_CASE(7) I8_PASS_CASE(8)
 #undef I8_PASS_CASE
-  set_error("no two-pass row-kernel instance for this plan");
+  set_error("no row-kernel (copy waves) instance for this plan");
   return I8CONV_BAD_ARGUMENT;
 }
 

@@ -261,12 +261,12 @@ bool plan_row(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
       break;
     }
   }
-  // 128 channels in 64-channel slices: the two-pass form when it fits
+  // 128 channels in 64-channel slices: the form with copy waves when it fits
   if (found && s.c == 128 && p->bn == 64 && rowpass_nfr(g.out_w) != 0 &&
       p->rows - 2 <= rowpass_max_rows(rowpass_nfr(g.out_w)) &&
       rowpass_lds_bytes(s.w + 2 * s.pad_w, p->rows - 2) <= size_t(kLdsBudget) &&
       g.output_elements * 4 <= INT32_MAX)
-    p->pass2 = true;
+    p->streamed = true;
   return found;
 }
 

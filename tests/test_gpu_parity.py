@@ -58,13 +58,16 @@ EDGE = {
     "dma_256x128_tails": lab.ConvShape(4, 63, 99, 128, 134, 3, 3, 1, 1, 1, 1, 1, 1),
     "dma_1x1_k62_short": lab.ConvShape(16, 56, 55, 256, 62, 1, 1, 0, 0, 1, 1, 1, 1),
     "dma_256x64_tails": lab.ConvShape(16, 57, 55, 128, 62, 3, 3, 1, 1, 1, 1, 1, 1),
-    # c == 128 3x3 stride 1: the two-pass row-streaming kernel.  Blocks of
-    # unequal height (8/7 and 2/1 output rows), a channel tail with scalar
-    # stores, four fragments per row, no padding.
-    "pass2_r8_uneven_k126": lab.ConvShape(32, 30, 30, 128, 126, 3, 3, 1, 1, 1, 1, 1, 1),
-    "pass2_r2_uneven": lab.ConvShape(8, 28, 28, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
-    "pass2_nfr4": lab.ConvShape(16, 20, 60, 128, 64, 3, 3, 1, 1, 1, 1, 1, 1),
-    "pass2_pad0": lab.ConvShape(4, 30, 30, 128, 64, 3, 3, 0, 0, 1, 1, 1, 1),
+    # c == 128 3x3 stride 1: the row-streaming kernel with copy waves.
+    # Blocks of unequal height (8/7 and 2/1 output rows), a channel tail with
+    # scalar stores, four fragments per row (the two-walk form, 5 plane
+    # copies per row: copy waves with 1 and 2 per row), one fragment per row
+    # (2 plane copies: copy waves with none), no padding.
+    "stream_r8_uneven_k126": lab.ConvShape(32, 30, 30, 128, 126, 3, 3, 1, 1, 1, 1, 1, 1),
+    "stream_r2_uneven": lab.ConvShape(8, 28, 28, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
+    "stream_nfr4": lab.ConvShape(16, 20, 60, 128, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    "stream_nfr1": lab.ConvShape(8, 14, 14, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
+    "stream_pad0": lab.ConvShape(4, 30, 30, 128, 64, 3, 3, 0, 0, 1, 1, 1, 1),
 }
 
 _expected_cache = {}
