@@ -43,7 +43,37 @@ def parse_args(argv: Optional[List[str]] = None) -> argparse.Namespace:
     p.add_argument("--range", default="baseline", choices=("baseline", "reference"),
                    help="data range: int8 full range (baseline) or U[-4,4] (reference)")
     p.add_argument("--driver", type=Path, default=DRIVER)
+    p.add_argument("--with-vendor", action="store_true",
+                   help="add vendor-library columns (sweep.py:44-56's --with-cudnn): MIOpen for "
+                        "every case (vendor_lab), hipBLASLt int8 GEMM for plain-GEMM layers")
+    p.add_argument("--vendor-driver", type=Path, default=None,
+                   help="vendor_lab binary (default: next to this file)")
     return p.parse_args(argv)
+
+
+def vendor_columns(args, configs: Path, case: str) -> dict:
+    """The comparison columns of one case: dispatch_ms (the dispatched
+    kernel, timed in the vendor driver's process), miopen_ms and its ratio,
+    and for plain-GEMM layers hipblaslt_ms and its ratio; *_correct says
+    whether the vendor output equals the dispatched kernel's."""
+    from . import vendor
+
+    driver = args.vendor_driver or vendor.VENDOR_DRIVER
+    row = vendor.miopen_row(configs, case, args.warmup, args.iterations, driver)
+    dispatch_ms = float(row["dispatch_ms"])
+    miopen_ms = float(row["vendor_ms"])
+    out = {"dispatch_ms": dispatch_ms,
+           "miopen_algo": row["vendor_algo"],
+           "miopen_ms": miopen_ms if miopen_ms > 0 else "",
+           "miopen_over_dispatch": miopen_ms / dispatch_ms if miopen_ms > 0 else "",
+           "miopen_correct": row["vendor_correct"],
+           "comparison_contract": row["comparison_contract"]}
+    from . import load_case
+    gemm = vendor.hipblaslt_gemm(load_case(str(configs), case), args.warmup, args.iterations)
+    out.update(gemm)
+    hb = gemm["hipblaslt_ms"]
+    out["hipblaslt_over_dispatch"] = float(hb) / dispatch_ms if hb != "" else ""
+    return out
 
 
 def requested_cases(configs: Path, cases: Optional[str]) -> List[str]:
@@ -75,13 +105,17 @@ def main(argv: Optional[List[str]] = None) -> int:
             sys.stderr.write(result.stdout + result.stderr)
             raise SystemExit(f"{case}: conv_lab exited with {result.returncode}")
         rows.append(next(csv.DictReader(result.stdout.splitlines())))
+        if args.with_vendor:
+            rows[-1].update(vendor_columns(args, configs, case))
         with args.output.open("w", newline="") as stream:
             writer = csv.DictWriter(stream, fieldnames=list(rows[0].keys()))
             writer.writeheader()
             writer.writerows(rows)
         r = rows[-1]
+        extra = (f"; miopen x{float(r['miopen_over_dispatch']):.1f}" if r.get("miopen_over_dispatch")
+                 else "")
         print(f"{case}: winner {r['winner']} dispatch {r['dispatch']} "
-              f"({r['tops']} TOPS); wrote {args.output}", flush=True)
+              f"({r['tops']} TOPS){extra}; wrote {args.output}", flush=True)
     return 0
 
 

@@ -2,7 +2,7 @@
 
 * registers the ``gpu`` marker (tests that need an MI355X);
 * puts the repository root on sys.path;
-* builds libi8conv.so / liboracle.so only when they are missing (the GPU box
+* builds libi8conv.so, the drivers and liboracle.so only when they are missing (the GPU box
   runs the prebuilt files and never builds).
 """
 import os
@@ -17,6 +17,7 @@ if ROOT not in sys.path:
 
 LIB = os.path.join(ROOT, "int8_kernel_lab_amd", "libi8conv.so")
 DRIVER = os.path.join(ROOT, "int8_kernel_lab_amd", "conv_lab")
+VENDOR = os.path.join(ROOT, "int8_kernel_lab_amd", "vendor_lab")
 ORACLE = os.path.join(ROOT, "oracle", "liboracle.so")
 
 
@@ -27,7 +28,7 @@ def pytest_configure(config):
 def _build_if_missing():
     if not os.path.exists(ORACLE):
         subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True)
-    if not (os.path.exists(LIB) and os.path.exists(DRIVER)):
+    if not (os.path.exists(LIB) and os.path.exists(DRIVER) and os.path.exists(VENDOR)):
         subprocess.run(["make", "-j8", "-C", os.path.join(ROOT, "int8_kernel_lab_amd", "csrc")],
                        check=True)
 

@@ -74,3 +74,27 @@ def test_sweep_over_reference_cases(tmp_path):
     for r in rows:
         assert r["generic_correct"] == "1" and r["winner"] != "none"
         assert r["dispatch"] in ("generic", "strip", "halo", "splitk")
+
+
+@pytest.mark.gpu
+def test_vendor_miopen_matches_dispatched_kernel():
+    # MIOpen's int8 convolution (an independent implementation) must write
+    # the same int32 output as the dispatched kernel on the same data
+    from int8_kernel_lab_amd import vendor
+    for case in ("cfg1_smoke", "cfg4b_k36_tail"):
+        say(f"[gpu] vendor_lab --case {case}")
+        row = vendor.miopen_row(os.path.join(ROOT, "int8_kernel_lab_amd", "workloads",
+                                             "baseline.csv"), case, warmup=1, iterations=3)
+        assert row["vendor_correct"] == "1", row
+        assert float(row["vendor_ms"]) > 0 and float(row["dispatch_ms"]) > 0
+
+
+@pytest.mark.gpu
+def test_vendor_hipblaslt_gemm_matches_dispatched_kernel():
+    import int8_kernel_lab_amd as lab
+    from int8_kernel_lab_amd import vendor
+    shape = lab.ConvShape(2, 28, 28, 64, 96, 1, 1, 0, 0, 1, 1, 1, 1)
+    say(f"[gpu] torch._int_mm vs dispatch on {shape}")
+    got = vendor.hipblaslt_gemm(shape, warmup=1, iterations=3)
+    assert got["hipblaslt_correct"] == 1, got
+    assert got["hipblaslt_ms"] > 0

@@ -128,3 +128,61 @@ def test_sweep_defaults():
     assert a.configs.name == "reference.csv" and a.iterations == 101 and a.warmup == 20
     assert a.strategy == "all"
     assert len(sweep.requested_cases(a.configs, None)) == 41
+
+
+# ---- vendor comparison columns (sweep.py:44-56's --with-cudnn) --------------
+
+FAKE_CONV_LAB = '''#!{py}
+import sys
+print("case,n,winner,dispatch,tops")
+print(sys.argv[sys.argv.index("--case") + 1] + ",1,halo,halo,1.5")
+'''
+
+FAKE_VENDOR_LAB = '''#!{py}
+import sys
+case = sys.argv[sys.argv.index("--case") + 1]
+print("case,dispatch,dispatch_ms,dispatch_batched_ms,vendor,vendor_algo,vendor_ms,"
+      "vendor_batched_ms,vendor_over_dispatch,vendor_correct,comparison_contract")
+print(case + ",halo,0.01,0.008,miopen,direct,0.5,0.49,50,1,\\"fake contract\\"")
+'''
+
+
+def _script(path, text):
+    path.write_text(text.format(py=sys.executable))
+    path.chmod(0o755)
+    return path
+
+
+def test_sweep_with_vendor_adds_comparison_columns(tmp_path):
+    conv = _script(tmp_path / "conv_lab", FAKE_CONV_LAB)
+    vend = _script(tmp_path / "vendor_lab", FAKE_VENDOR_LAB)
+    out = tmp_path / "sweep.csv"
+    assert sweep.main(["--cases", "smoke,batch16_bottleneck_reduce", "--driver", str(conv),
+                       "--with-vendor", "--vendor-driver", str(vend), "--output", str(out)]) == 0
+    import csv
+    rows = list(csv.DictReader(out.open()))
+    assert [r["case"] for r in rows] == ["smoke", "batch16_bottleneck_reduce"]
+    for r in rows:
+        assert float(r["dispatch_ms"]) == 0.01 and float(r["miopen_ms"]) == 0.5
+        assert float(r["miopen_over_dispatch"]) == pytest.approx(50.0)
+        assert r["miopen_correct"] == "1" and r["comparison_contract"] == "fake contract"
+    # 3x3 smoke is not a plain GEMM; the 1x1 bottleneck is, but there is no GPU here
+    assert rows[0]["hipblaslt_contract"].startswith("not a plain gemm")
+    assert rows[1]["hipblaslt_contract"] == "no gpu" and rows[1]["hipblaslt_ms"] == ""
+
+
+def test_vendor_plain_gemm_predicate():
+    from int8_kernel_lab_amd import vendor
+    assert vendor.is_plain_gemm(lab.ConvShape(64, 56, 56, 256, 64, 1, 1, 0, 0, 1, 1, 1, 1))
+    assert not vendor.is_plain_gemm(lab.ConvShape(1, 16, 16, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1))
+    assert not vendor.is_plain_gemm(lab.ConvShape(1, 16, 16, 64, 64, 1, 1, 0, 0, 2, 2, 1, 1))
+    assert not vendor.is_plain_gemm(lab.ConvShape(1, 16, 16, 64, 64, 1, 1, 1, 1, 1, 1, 1, 1))
+
+
+def test_vendor_driver_is_built_and_links():
+    # the MIOpen comparison driver links against libi8conv and MIOpen; its
+    # usage error needs no GPU
+    from int8_kernel_lab_amd import vendor
+    assert vendor.VENDOR_DRIVER.exists()
+    r = subprocess.run([str(vendor.VENDOR_DRIVER), "--bogus"], text=True, capture_output=True)
+    assert r.returncode != 0 and "usage: vendor_lab" in r.stderr
