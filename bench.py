@@ -88,6 +88,53 @@ def write_floor(workload: str, steps: int, warmup: int) -> int:
     return 0
 
 
+def requant_bench(workload: str, steps: int, warmup: int) -> int:
+    """The same layer with requantized int8 output (i8conv_launch_requant:
+    the dispatched kernel's fused epilogue where it has one, else the int32
+    convolution into a workspace and a requantizing pass), checked against
+    the oracle, then timed like the headline (i8conv_measure_requant: events
+    around `steps` back-to-back launches on the launch stream, in C++).  A
+    separate line, not the headline: the reference's contract is int32
+    output."""
+    import numpy as np
+    import int8_kernel_lab_amd as lab
+    from oracle import oracle
+
+    shape = lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), workload)
+    g = shape.geometry()
+    x, w, b = lab.make_case_data(shape)
+    rng = np.random.default_rng(1)
+    mult = rng.integers(2 ** 30, 2 ** 31, size=shape.k).astype(np.int32)
+    shift = rng.integers(50, 54, size=shape.k).astype(np.int32)
+    bufs = [lab.DeviceBuffer.from_array(a) for a in (x, w, b, mult, shift)]
+    yb = lab.DeviceBuffer(g.output_elements)
+    ws_n = lab.requant_workspace_bytes(shape)
+    ws = lab.DeviceBuffer(ws_n) if ws_n else None
+    yb.fill(0xA5)
+    lab.launch_requant(shape, *bufs, 3, yb, ws, ws_n)
+    lab.synchronize()
+    got = yb.download(np.int8, g.output_elements).reshape(shape.output_shape)
+    if not np.array_equal(got, oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, 3)):
+        print(f"bench.py: requantized output differs from the oracle on {workload}", file=sys.stderr)
+        return 1
+    median_ms, mean_ms = lab.measure_requant(shape, *bufs, 3, yb, ws, ws_n, warmup=warmup,
+                                             iterations=steps)
+    us = mean_ms * 1e3
+    nbytes = shape.algorithmic_bytes() - 4 * g.output_elements + g.output_elements + 8 * shape.k
+    print(json.dumps({"requant_workload": workload, "fused": lab.requant_fused(shape),
+                      "us_per_launch": round(us, 3),
+                      "per_launch_median_us": round(median_ms * 1e3, 3),
+                      "tops": round(shape.ops() / (us * 1e-6) / 1e12, 1),
+                      "pct_int8_mfma_peak": round(100 * shape.ops() / (us * 1e-6) / 1e12
+                                                  / PEAK_INT8_TOPS, 2),
+                      "algorithmic_bytes": nbytes,
+                      "gbps": round(nbytes / (us * 1e-6) / 1e9, 1), "launches": steps}), flush=True)
+    for buf in bufs + [yb, ws]:
+        if buf is not None:
+            buf.close()
+    return 0
+
+
 def traffic_record(workload: str, kernel: str):
     """HBM bytes per launch of `kernel` on `workload` from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.json),
@@ -118,7 +165,12 @@ def main() -> int:
     ap.add_argument("--write-floor", action="store_true",
                     help="instead of the benchmark, time a plain fill kernel writing exactly "
                          "the workload's int32 output bytes (the store traffic alone)")
+    ap.add_argument("--requant", action="store_true",
+                    help="instead of the benchmark, time the same layer with requantized int8 "
+                         "output (a separate line; the headline contract is int32 output)")
     args = ap.parse_args()
+    if args.requant:
+        return requant_bench(args.workload, args.steps, args.warmup)
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration, args.steps)
     if args.write_floor:

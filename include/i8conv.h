@@ -140,6 +140,42 @@ int i8conv_launch_dispatched(const i8conv_shape *shape, const int8_t *input,
                              int32_t *output, void *workspace,
                              size_t workspace_bytes, void *stream);
 
+/* ---- requantized int8 output (the step after the path) ---------------- */
+
+/* No counterpart in the reference: its vendor comparison writes INT8 output
+ * (README.md:89-90, cudnn_legacy.cuh:40-41) but it has no requantizing code.
+ * The lab's definition, per output channel k:
+ *   y = clamp(zero_point + round(acc * mult[k] / 2^shift[k]), -128, 127)
+ * with acc the int32 convolution (bias included), shift[k] clamped to
+ * [0, 62], the product exact in int64 and ties rounded away from zero.
+ * mult and shift are device arrays of K int32; the output is NHWK int8. */
+
+/* Requantizes an int32 [pixels][channels] tensor into int8 (asynchronous). */
+int i8conv_requantize(const int32_t *acc, int64_t pixels, int32_t channels,
+                      const int32_t *mult, const int32_t *shift,
+                      int32_t zero_point, int8_t *output, void *stream);
+/* 1 when the dispatched kernel for `shape` requantizes in its own epilogue
+ * (no int32 tensor is written), 0 when the convolution goes through an
+ * int32 workspace and a requantizing pass. */
+int i8conv_requant_fused(const i8conv_shape *shape);
+/* Workspace i8conv_launch_requant needs: the dispatched kernel's, plus the
+ * int32 output (256-byte aligned) when the requantization is not fused. */
+size_t i8conv_requant_workspace_bytes(const i8conv_shape *shape);
+/* The dispatched convolution with int8 output: fused epilogue or
+ * convolution into the workspace + requantizing pass.  Allocates nothing. */
+int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input,
+                          const int8_t *filter, const int32_t *bias,
+                          const int32_t *mult, const int32_t *shift,
+                          int32_t zero_point, int8_t *output, void *workspace,
+                          size_t workspace_bytes, void *stream);
+/* i8conv_measure (below) around i8conv_launch_requant. */
+int i8conv_measure_requant(const i8conv_shape *shape, const int8_t *input,
+                           const int8_t *filter, const int32_t *bias,
+                           const int32_t *mult, const int32_t *shift,
+                           int32_t zero_point, int8_t *output, void *workspace,
+                           size_t workspace_bytes, void *stream, int warmup,
+                           int iterations, float *median_ms, float *batched_ms);
+
 /* ---- thin HIP runtime layer used by the host driver -------------------- */
 
 /* DeviceBuffer (conv_lab.cu:24-37) as C calls. */

@@ -35,7 +35,8 @@ __all__ = [
     "launch_generic", "launch_spatial_strip", "load_case", "load_workloads",
     "make_case_data", "measure", "spatial_strip_eligible", "workspace_bytes",
     "WORKLOADS_DIR", "BASELINE_SEED", "device_count", "device_info", "set_device",
-    "synchronize",
+    "synchronize", "requantize", "requant_fused", "requant_workspace_bytes", "launch_requant",
+    "conv2d_requant", "measure_requant",
 ]
 
 KERNELS = ("generic", "strip", "halo", "splitk")
@@ -353,3 +354,70 @@ def conv2d(input: np.ndarray, filter: np.ndarray, bias: np.ndarray, shape: ConvS
         for b in (xb, wb, bb, yb, ws):
             if b is not None:
                 b.close()
+
+
+# ---- requantized int8 output (no reference counterpart; README.md:89-90) ----
+
+def requant_fused(shape: ConvShape) -> bool:
+    """Whether the dispatched kernel requantizes in its own epilogue."""
+    return bool(lib().i8conv_requant_fused(ctypes.byref(shape.c_struct())))
+
+
+def requant_workspace_bytes(shape: ConvShape) -> int:
+    return int(lib().i8conv_requant_workspace_bytes(ctypes.byref(shape.c_struct())))
+
+
+def requantize(acc, pixels: int, channels: int, mult, shift, zero_point: int, output,
+               stream=None) -> None:
+    """Asynchronous int32 -> int8 requantization of device tensors:
+    y = clamp(zero_point + round(acc * mult[k] / 2^shift[k]), -128, 127)."""
+    check(lib().i8conv_requantize(_ptr(acc), int(pixels), int(channels), _ptr(mult), _ptr(shift),
+                                  int(zero_point), _ptr(output), _ptr(stream)), "requantize")
+
+
+def launch_requant(shape: ConvShape, input, filter, bias, mult, shift, zero_point: int, output,
+                   workspace=None, workspace_nbytes: int = 0, stream=None) -> None:
+    """The dispatched convolution with requantized NHWK int8 output."""
+    if isinstance(workspace, DeviceBuffer) and not workspace_nbytes:
+        workspace_nbytes = workspace.nbytes
+    check(lib().i8conv_launch_requant(ctypes.byref(shape.c_struct()), _ptr(input), _ptr(filter),
+                                      _ptr(bias), _ptr(mult), _ptr(shift), int(zero_point),
+                                      _ptr(output), _ptr(workspace), int(workspace_nbytes),
+                                      _ptr(stream)), "launch_requant")
+
+
+def conv2d_requant(input: np.ndarray, filter: np.ndarray, bias: np.ndarray, mult: np.ndarray,
+                   shift: np.ndarray, zero_point: int, shape: ConvShape) -> np.ndarray:
+    """The dispatched convolution with int8 output, on host arrays: allocates,
+    copies, launches, synchronizes, returns NHWK int8."""
+    g = shape.geometry()
+    bufs = [DeviceBuffer.from_array(np.ascontiguousarray(a, dtype=t))
+            for a, t in ((input, np.int8), (filter, np.int8), (bias, np.int32),
+                         (mult, np.int32), (shift, np.int32))]
+    yb = DeviceBuffer(max(1, g.output_elements))
+    ws_n = requant_workspace_bytes(shape)
+    ws = DeviceBuffer(ws_n) if ws_n else None
+    try:
+        launch_requant(shape, *bufs[:5], zero_point, yb, ws, ws_n)
+        synchronize()
+        return yb.download(np.int8, g.output_elements).reshape(shape.output_shape)
+    finally:
+        for b in bufs + [yb, ws]:
+            if b is not None:
+                b.close()
+
+
+def measure_requant(shape: ConvShape, input, filter, bias, mult, shift, zero_point: int, output,
+                    workspace=None, workspace_nbytes: int = 0, warmup: int = 20,
+                    iterations: int = 101, stream=None) -> Tuple[float, float]:
+    """measure() (conv_lab.cu:88-110) around launch_requant, timed in C++:
+    (median ms per launch, mean ms of back-to-back launches)."""
+    if isinstance(workspace, DeviceBuffer) and not workspace_nbytes:
+        workspace_nbytes = workspace.nbytes
+    med, bat = ctypes.c_float(), ctypes.c_float()
+    check(lib().i8conv_measure_requant(ctypes.byref(shape.c_struct()), _ptr(input), _ptr(filter),
+                                       _ptr(bias), _ptr(mult), _ptr(shift), int(zero_point),
+                                       _ptr(output), _ptr(workspace), int(workspace_nbytes),
+                                       _ptr(stream), int(warmup), int(iterations),
+                                       ctypes.byref(med), ctypes.byref(bat)), "measure_requant")
+    return med.value, bat.value

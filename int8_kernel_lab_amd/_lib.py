@@ -60,6 +60,16 @@ SIGNATURES = {
     "i8conv_spatial_strip_eligible": (c_int, [POINTER(CShape)]),
     "i8conv_launch_dispatched": (c_int, [POINTER(CShape), c_void_p, c_void_p, c_void_p,
                                          c_void_p, c_void_p, c_size_t, c_void_p]),
+    "i8conv_requantize": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
+                                  c_void_p, c_void_p]),
+    "i8conv_requant_fused": (c_int, [POINTER(CShape)]),
+    "i8conv_requant_workspace_bytes": (c_size_t, [POINTER(CShape)]),
+    "i8conv_launch_requant": (c_int, [POINTER(CShape), c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_void_p, c_int32, c_void_p, c_void_p, c_size_t,
+                                      c_void_p]),
+    "i8conv_measure_requant": (c_int, [POINTER(CShape), c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p,
+                                       c_int, c_int, POINTER(c_float), POINTER(c_float)]),
     "i8conv_device_count": (c_int, [POINTER(c_int)]),
     "i8conv_set_device": (c_int, [c_int]),
     "i8conv_device_alloc": (c_int, [POINTER(c_void_p), c_size_t]),

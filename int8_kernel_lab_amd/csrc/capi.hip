@@ -23,6 +23,60 @@ int hip_fail(const char *what, hipError_t e) {
 bool aligned(const void *p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
+// measure() of conv_lab.cu:88-110 around any launch: `warmup` launches,
+// synchronize, then `iterations` launches each bracketed by its own event
+// pair on `stream` and synchronized (median), plus `iterations` back-to-back
+// launches between one event pair (mean per launch).
+template <class Launch>
+int measure_loop(Launch launch, void *stream, int warmup, int iterations, float *median_ms,
+                 float *batched_ms) {
+  if (warmup < 0 || iterations <= 0 || !median_ms) {
+    set_error("measure needs warmup >= 0, iterations > 0 and an output");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int i = 0; i < warmup; ++i) {
+    const int rc = launch();
+    if (rc != I8CONV_OK) return rc;
+  }
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail("warmup", e);
+  hipEvent_t start, stop;
+  if ((e = hipEventCreate(&start)) != hipSuccess) return hip_fail("hipEventCreate", e);
+  if ((e = hipEventCreate(&stop)) != hipSuccess) {
+    (void)hipEventDestroy(start);
+    return hip_fail("hipEventCreate", e);
+  }
+  int rc = I8CONV_OK;
+  std::vector<float> samples;
+  samples.reserve(size_t(iterations));
+  for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) {
+    float ms = 0.f;
+    if ((e = hipEventRecord(start, s)) != hipSuccess) { rc = hip_fail("hipEventRecord", e); break; }
+    if ((rc = launch()) != I8CONV_OK) break;
+    if ((e = hipEventRecord(stop, s)) != hipSuccess) { rc = hip_fail("hipEventRecord", e); break; }
+    if ((e = hipEventSynchronize(stop)) != hipSuccess) { rc = hip_fail("hipEventSynchronize", e); break; }
+    if ((e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) { rc = hip_fail("hipEventElapsedTime", e); break; }
+    samples.push_back(ms);
+  }
+  if (rc == I8CONV_OK) {
+    std::sort(samples.begin(), samples.end());
+    *median_ms = samples[samples.size() / 2];
+  }
+  if (rc == I8CONV_OK && batched_ms) {
+    float ms = 0.f;
+    if ((e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+    for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch();
+    if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+    if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
+    if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) rc = hip_fail("hipEventElapsedTime", e);
+    if (rc == I8CONV_OK) *batched_ms = ms / float(iterations);
+  }
+  // teardown: a failure here cannot change the measured result
+  (void)hipEventDestroy(start);
+  (void)hipEventDestroy(stop);
+  return rc;
+}
 }  // namespace
 
 void set_error(const std::string &message) { g_last_error = message; }
@@ -231,6 +285,94 @@ int i8conv_launch_dispatched(const i8conv_shape *shape, const int8_t *input,
                        workspace_bytes, stream);
 }
 
+// ---- requantized int8 output -------------------------------------------------
+
+namespace {
+// The dispatched plan when it is the row kernel with copy waves, whose
+// epilogue requantizes.
+bool fused_requant_plan(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *pp) {
+  return dispatch(s) == I8CONV_KERNEL_HALO && plan_halo(s, g, pp) && pp->row && pp->streamed;
+}
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+}  // namespace
+
+int i8conv_requantize(const int32_t *acc, int64_t pixels, int32_t channels,
+                      const int32_t *mult, const int32_t *shift, int32_t zero_point,
+                      int8_t *output, void *stream) {
+  if (pixels < 0 || channels <= 0) {
+    set_error("requantize: pixels must be >= 0 and channels > 0");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  if (pixels > 0 && (!acc || !mult || !shift || !output)) {
+    set_error("requantize: null tensor pointer");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  if (!aligned(acc, 4) || !aligned(mult, 4) || !aligned(shift, 4)) {
+    set_error("requantize: acc, mult and shift must be 4-byte aligned");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  return launch_requant(acc, pixels, channels, mult, shift, zero_point, output, stream);
+}
+
+int i8conv_requant_fused(const i8conv_shape *shape) {
+  if (!shape) return 0;
+  i8conv_geometry g;
+  if (derive(*shape, &g) != I8CONV_OK) return 0;
+  PatchPlan pp;
+  return fused_requant_plan(*shape, g, &pp) ? 1 : 0;
+}
+
+size_t i8conv_requant_workspace_bytes(const i8conv_shape *shape) {
+  if (!shape) return 0;
+  i8conv_geometry g;
+  if (derive(*shape, &g) != I8CONV_OK) return 0;
+  if (i8conv_requant_fused(shape)) return i8conv_dispatch_workspace_bytes(shape);
+  return align256(size_t(g.output_elements) * 4) + i8conv_dispatch_workspace_bytes(shape);
+}
+
+int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input, const int8_t *filter,
+                          const int32_t *bias, const int32_t *mult, const int32_t *shift,
+                          int32_t zero_point, int8_t *output, void *workspace,
+                          size_t workspace_bytes, void *stream) {
+  if (!shape) {
+    set_error("null shape");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  i8conv_geometry g;
+  const int rc = derive(*shape, &g);
+  if (rc != I8CONV_OK) return rc;
+  if (!input || !filter || !bias || !mult || !shift || !output) {
+    set_error("null tensor pointer");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  if (!aligned(input, 16) || !aligned(filter, 16) || !aligned(bias, 4) || !aligned(mult, 4) ||
+      !aligned(shift, 4)) {
+    set_error("input/filter must be 16-byte aligned, bias/mult/shift 4-byte aligned");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  const int id = dispatch(*shape);
+  PatchPlan pp;
+  if (id == I8CONV_KERNEL_HALO && plan_halo(*shape, g, &pp) && pp.row && pp.streamed) {
+    // fused: the output is < 2 GiB (the plan checks it)
+    const ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
+    const RequantArgs q{mult, shift, zero_point, output};
+    return launch_rowpass(args, pp, stream, &q);
+  }
+  const size_t acc_bytes = align256(size_t(g.output_elements) * 4);
+  const size_t need = acc_bytes + i8conv_workspace_bytes(id, shape);
+  if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) {
+    set_error("requantized launch needs a 256-byte aligned workspace of " + std::to_string(need) +
+              " bytes");
+    return I8CONV_WORKSPACE_TOO_SMALL;
+  }
+  int32_t *acc = static_cast<int32_t *>(workspace);
+  void *conv_ws = static_cast<char *>(workspace) + acc_bytes;
+  const int r = i8conv_launch(id, shape, input, filter, bias, acc, conv_ws,
+                              workspace_bytes - acc_bytes, stream);
+  if (r != I8CONV_OK) return r;
+  return launch_requant(acc, g.gemm_m, g.gemm_n, mult, shift, zero_point, output, stream);
+}
+
 // ---- runtime layer -------------------------------------------------------
 
 int i8conv_device_count(int *count) {
@@ -320,56 +462,25 @@ int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
                    void *workspace, size_t workspace_bytes, void *stream,
                    int warmup, int iterations, float *median_ms,
                    float *batched_ms) {
-  if (warmup < 0 || iterations <= 0 || !median_ms) {
-    set_error("measure needs warmup >= 0, iterations > 0 and an output");
-    return I8CONV_BAD_ARGUMENT;
-  }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  auto launch = [&]() {
-    return i8conv_launch(id, shape, input, filter, bias, output, workspace,
-                         workspace_bytes, stream);
-  };
-  for (int i = 0; i < warmup; ++i) {
-    const int rc = launch();
-    if (rc != I8CONV_OK) return rc;
-  }
-  hipError_t e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return hip_fail("warmup", e);
-  hipEvent_t start, stop;
-  if ((e = hipEventCreate(&start)) != hipSuccess) return hip_fail("hipEventCreate", e);
-  if ((e = hipEventCreate(&stop)) != hipSuccess) {
-    (void)hipEventDestroy(start);
-    return hip_fail("hipEventCreate", e);
-  }
-  int rc = I8CONV_OK;
-  std::vector<float> samples;
-  samples.reserve(size_t(iterations));
-  for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) {
-    float ms = 0.f;
-    if ((e = hipEventRecord(start, s)) != hipSuccess) { rc = hip_fail("hipEventRecord", e); break; }
-    if ((rc = launch()) != I8CONV_OK) break;
-    if ((e = hipEventRecord(stop, s)) != hipSuccess) { rc = hip_fail("hipEventRecord", e); break; }
-    if ((e = hipEventSynchronize(stop)) != hipSuccess) { rc = hip_fail("hipEventSynchronize", e); break; }
-    if ((e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) { rc = hip_fail("hipEventElapsedTime", e); break; }
-    samples.push_back(ms);
-  }
-  if (rc == I8CONV_OK) {
-    std::sort(samples.begin(), samples.end());
-    *median_ms = samples[samples.size() / 2];
-  }
-  if (rc == I8CONV_OK && batched_ms) {
-    float ms = 0.f;
-    if ((e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-    for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch();
-    if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-    if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
-    if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) rc = hip_fail("hipEventElapsedTime", e);
-    if (rc == I8CONV_OK) *batched_ms = ms / float(iterations);
-  }
-  // teardown: a failure here cannot change the measured result
-  (void)hipEventDestroy(start);
-  (void)hipEventDestroy(stop);
-  return rc;
+  return measure_loop(
+      [&]() {
+        return i8conv_launch(id, shape, input, filter, bias, output, workspace,
+                             workspace_bytes, stream);
+      },
+      stream, warmup, iterations, median_ms, batched_ms);
+}
+
+int i8conv_measure_requant(const i8conv_shape *shape, const int8_t *input, const int8_t *filter,
+                           const int32_t *bias, const int32_t *mult, const int32_t *shift,
+                           int32_t zero_point, int8_t *output, void *workspace,
+                           size_t workspace_bytes, void *stream, int warmup, int iterations,
+                           float *median_ms, float *batched_ms) {
+  return measure_loop(
+      [&]() {
+        return i8conv_launch_requant(shape, input, filter, bias, mult, shift, zero_point, output,
+                                     workspace, workspace_bytes, stream);
+      },
+      stream, warmup, iterations, median_ms, batched_ms);
 }
 
 const char *i8conv_status_string(int status) {

@@ -86,6 +86,22 @@ struct ConvArgs {
   int splits;
 };
 
+// The lab's int32 -> int8 requantization of one value:
+//   clamp(zp + round(acc * mult / 2^shift), -128, 127)
+// with shift clamped to [0, 62], the product exact in int64 (|acc|, |mult|
+// <= 2^31, so |p| <= 2^62) and ties rounded away from zero:
+//   round(p / 2^s) = floor((p + 2^(s-1) - [p < 0]) / 2^s)   (s >= 1)
+// (for p < 0, -floor((|p| + h) / 2^s) = floor((p + h - 1) / 2^s) with
+// h = 2^(s-1)), one add and one arithmetic shift.  Host and device: a CPU
+// test checks it against the checker's own restatement.
+I8_HD inline int32_t requant1(int32_t acc, int32_t mult, int32_t shift, int32_t zp) {
+  const int s = shift < 0 ? 0 : (shift > 62 ? 62 : shift);
+  const int64_t p = int64_t(acc) * int64_t(mult);
+  const int64_t h = s > 0 ? (int64_t(1) << (s - 1)) - (p < 0 ? 1 : 0) : 0;
+  const int64_t q = ((p + h) >> s) + zp;
+  return int32_t(q < -128 ? -128 : (q > 127 ? 127 : q));
+}
+
 #if defined(__HIPCC__)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -210,6 +226,16 @@ __device__ __forceinline__ OutWindow out_window(int32_t *y, int64_t gemm_m, int 
   return w;
 }
 __device__ __forceinline__ void store_out1(int32_t *dst, int32_t v) { *dst = v; }
+
+// Four consecutive channels requantized and packed into one dword (byte e =
+// channel e, the NHWK int8 order).
+__device__ __forceinline__ uint32_t requant4(v4i acc, v4i mult, v4i shift, int32_t zp) {
+  uint32_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    packed |= (uint32_t(requant1(acc[e], mult[e], shift[e], zp)) & 0xffu) << (8 * e);
+  return packed;
+}
 
 // D = A x B + C over int8 -> int32.  A is 16 rows (lane % 16) by 64 k,
 // B is 64 k by 16 columns (lane % 16); lane l supplies 16 k-bytes of its

@@ -86,7 +86,20 @@ int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stre
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream);
-int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream);
+// Requantized int8 output (kernel_requant.hip): per output channel k,
+// y = clamp(zero_point + round(acc * mult[k] / 2^shift[k]), -128, 127).
+struct RequantArgs {
+  const int32_t *mult;
+  const int32_t *shift;
+  int32_t zero_point;
+  int8_t *y;  // NHWK int8
+};
+int launch_requant(const int32_t *acc, int64_t pixels, int32_t channels, const int32_t *mult,
+                   const int32_t *shift, int32_t zero_point, int8_t *out, void *stream);
+// q == nullptr: int32 output to a.y; else the requantized int8 output to
+// q->y, computed in the kernel's epilogue (a.y unused)
+int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream,
+                   const RequantArgs *q = nullptr);
 // kernel_rowpass.hip: fragments per output row of its instance for out_w
 // (0: none), and its LDS bytes for wp padded columns and `rows` output rows
 int rowpass_nfr(int out_w);

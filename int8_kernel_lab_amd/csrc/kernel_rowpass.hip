@@ -60,6 +60,11 @@ struct PassArgs {
   int32_t *y;
   uint32_t x_bytes, w_bytes;
   uint32_t y_bytes;  // output bytes (< 2^31: checked at launch)
+  // requantized int8 output (kQ instances): per-channel multiplier and
+  // shift, zero point, output (y_bytes then counts int8 bytes)
+  const int32_t *qmult, *qshift;
+  int8_t *qy;
+  int32_t qzp;
   int n, h, wd, c, pad_h, pad_w;
   int out_h, out_w, gemm_n, gemm_k;
   int hp, wp;        // padded rows per image, padded columns
@@ -101,7 +106,7 @@ __device__ __forceinline__ void flag_wait(uint32_t addr, int target) {
 // Per-MFMA-wave state of a row walk over NG channel groups at a time: NG ==
 // 1 walks the rows twice (group 0, then group 1; the two-pass form), NG == 2
 // once with both groups per row (the single-pass form).
-template <int R, int NFR, int NG>
+template <int R, int NFR, int NG, bool kQ>
 struct PassState {
   v4i wf[NG][kTaps];       // this wave's 16 channels, the walk's groups, all taps (t = fy*3 + fx)
   v4i acc[R][NFR];         // output rows of the block
@@ -120,6 +125,8 @@ struct PassState {
   __amdgpu_buffer_rsrc_t yr;
   uint32_t voff[NFR];
   uint32_t row_stride;
+  // kQ: this lane's four channels' multiplier and shift
+  v4i qm, qs;
 
   template <int G>
   __device__ __forceinline__ void load_row(const PassArgs &p, int r) {
@@ -200,13 +207,36 @@ struct PassState {
   }
 
   // Output row O: the accumulators already hold bias + dot products.  N % 4
-  // == 0 (and a 16-byte aligned output): one 16-byte buffer store per
-  // fragment (write-through, kStoreThrough) at a scalar row offset, no
-  // address arithmetic; otherwise element stores.
+  // == 0 (and an aligned output): one buffer store per fragment at a scalar
+  // row offset, no address arithmetic: 16 bytes of int32 (write-through,
+  // kStoreThrough), or with kQ the four requantized int8 values as one
+  // dword (evict-first, kStoreStream: a wave writes 16 bytes of a pixel's
+  // line, and the L2 merges the four waves' pieces before writing it);
+  // otherwise element stores.
   template <int O>
   __device__ __forceinline__ void store_row(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                             int oc0, int lane) {
     if (O >= rows_out) return;
+    if constexpr (kQ) {
+      if (vec) {
+#pragma unroll
+        for (int j = 0; j < NFR; ++j)
+          __builtin_amdgcn_raw_buffer_store_b32(requant4(acc[O][j], qm, qs, p.qzp), yr, voff[j],
+                                                O * row_stride, kStoreStream);
+        return;
+      }
+      const int m_row = m_row0 + O * p.out_w;
+#pragma unroll
+      for (int j = 0; j < NFR; ++j) {
+        const int col = 16 * j + (lane & 15);
+        if (col >= p.out_w) continue;
+        int8_t *dst = p.qy + size_t(m_row + col) * size_t(p.gemm_n) + oc0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (oc0 + e < p.gemm_n) dst[e] = int8_t(requant1(acc[O][j][e], qm[e], qs[e], p.qzp));
+      }
+      return;
+    }
     if (vec) {
 #pragma unroll
       for (int j = 0; j < NFR; ++j)
@@ -313,7 +343,7 @@ struct CopySchedule {
   }
 };
 
-template <int R, int NFR, int NG>
+template <int R, int NFR, int NG, bool kQ>
 __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
   const PassArgs p = p_arg;
@@ -336,7 +366,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
 
   // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows]
   //      [filter halves: 18 KB per wave][chunk counters]
-  PassState<R, NFR, NG> st;
+  PassState<R, NFR, NG, kQ> st;
   st.bias_lds = smem + wave * 256;
   st.planes = smem + kHaloBiasLds;
   st.plane_bytes = p.plane_copies * 1024;
@@ -423,15 +453,28 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     }
   const int m_row0 = (b * p.out_h + oy0) * p.out_w;
   const int oc0 = tile_n + wave * 16 + 4 * (lane >> 4);
-  const bool vec = (p.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(p.y) & 15) == 0;
-  st.yr = make_rsrc(p.y, p.y_bytes);
-  st.row_stride = uint32_t(p.out_w) * uint32_t(p.gemm_n) * 4u;
+  // output element size: 4 (int32) or 1 (requantized int8)
+  constexpr uint32_t esize = kQ ? 1u : 4u;
+  const void *ybase = kQ ? static_cast<const void *>(p.qy) : static_cast<const void *>(p.y);
+  const bool vec = (p.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(ybase) & (4 * esize - 1)) == 0;
+  st.yr = make_rsrc(ybase, p.y_bytes);
+  st.row_stride = uint32_t(p.out_w) * uint32_t(p.gemm_n) * esize;
 #pragma unroll
   for (int j = 0; j < NFR; ++j) {
     const int col = 16 * j + (lane & 15);
     st.voff[j] = col < p.out_w && oc0 < p.gemm_n
-                     ? (uint32_t(m_row0 + col) * uint32_t(p.gemm_n) + uint32_t(oc0)) * 4u
+                     ? (uint32_t(m_row0 + col) * uint32_t(p.gemm_n) + uint32_t(oc0)) * esize
                      : kOutOfRange;
+  }
+  if constexpr (kQ) {
+    // channels past N read as zero (their values are never stored)
+    const auto mr = make_rsrc(p.qmult, uint32_t(p.gemm_n) * 4u);
+    const auto sr = make_rsrc(p.qshift, uint32_t(p.gemm_n) * 4u);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      st.qm[e] = __builtin_amdgcn_raw_buffer_load_b32(mr, uint32_t(oc0 + e) * 4u, 0, 0);
+      st.qs[e] = __builtin_amdgcn_raw_buffer_load_b32(sr, uint32_t(oc0 + e) * 4u, 0, 0);
+    }
   }
 
   st.template walk<0>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
@@ -440,9 +483,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   st.template store_row<R - 1>(p, vec, rows_out, m_row0, oc0, lane);
 }
 
-template <int R, int NFR>
-int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
-  auto kern = rowpass_kernel<R, NFR, walk_groups(NFR)>;
+template <int R, int NFR, bool kQ>
+int launch_q(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
+  auto kern = rowpass_kernel<R, NFR, walk_groups(NFR), kQ>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -459,6 +502,12 @@ int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
     return I8CONV_HIP_ERROR;
   }
   return I8CONV_OK;
+}
+
+template <int R, int NFR>
+int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s, bool requant) {
+  return requant ? launch_q<R, NFR, true>(h, blocks, lds, s)
+                 : launch_q<R, NFR, false>(h, blocks, lds, s);
 }
 
 }  // namespace
@@ -480,7 +529,7 @@ size_t rowpass_lds_bytes(int wp, int rows) {
          size_t(4) * kHalves * 1024 + 128;  // + chunk counters (2 x up to 10 rows)
 }
 
-int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
+int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream, const RequantArgs *q) {
   const int R = p.rows - 2;
   const int nfr = rowpass_nfr(a.out_w);
   const int wp = a.wd + 2 * a.pad_w;
@@ -502,7 +551,13 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
   h.y = a.y;
   h.x_bytes = a.x_bytes;
   h.w_bytes = a.w_bytes;
-  h.y_bytes = uint32_t(int64_t(a.gemm_m) * a.gemm_n * 4);
+  h.y_bytes = uint32_t(int64_t(a.gemm_m) * a.gemm_n * (q ? 1 : 4));
+  if (q) {
+    h.qmult = q->mult;
+    h.qshift = q->shift;
+    h.qy = q->y;
+    h.qzp = q->zero_point;
+  }
   h.n = a.n;
   h.h = a.h;
   h.wd = a.wd;
@@ -527,9 +582,9 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define I8_PASS_CASE(RR)                                                   \
   if (R == RR) {                                                           \
-    if (nfr == 1) return launch_t<RR, 1>(h, grid, lds, s);                 \
-    if (nfr == 2) return launch_t<RR, 2>(h, grid, lds, s);                 \
-    if constexpr (RR <= 4) return launch_t<RR, 4>(h, grid, lds, s);        \
+    if (nfr == 1) return launch_t<RR, 1>(h, grid, lds, s, q != nullptr);   \
+    if (nfr == 2) return launch_t<RR, 2>(h, grid, lds, s, q != nullptr);   \
+    if constexpr (RR <= 4) return launch_t<RR, 4>(h, grid, lds, s, q != nullptr); \
   }
   I8_PASS_CASE(1) I8_PASS_CASE(2) I8_PASS_CASE(3) I8_PASS_CASE(4)
   I8_PASS_CASE(5) I8_PASS_CASE(6) I8_PASS_CASE(7) I8_PASS_CASE(8)

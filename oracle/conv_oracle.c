@@ -13,6 +13,9 @@
  *   oracle_conv              reference_value over every output index
  *   oracle_validate_sampled  src/conv_lab.cu:68-86 (sampling rule)
  *   oracle_strip_eligible_reference  include/spatial_strip.cuh:11-15
+ *   oracle_requantize        the lab's int32 -> int8 requantization (no
+ *                            reference code: the reference's vendor path
+ *                            writes INT8, README.md:89-90; see below)
  * Accumulation is int32 with two's-complement wrap (done in uint32 so that
  * wrap is defined C), the same as the reference's int32 `sum += x * w` for
  * every input that does not overflow and the same as the MFMA accumulator.
@@ -157,4 +160,35 @@ int oracle_strip_eligible_reference(const oracle_shape *s) {
   if (oracle_derive(s, &g)) return 0;
   return s->r == 3 && s->s == 3 && s->stride_w == 1 && s->dilation_w == 1 &&
          s->c % 64 == 0 && s->k % 64 == 0 && g.out_w % 128 == 0;
+}
+
+/*
+ * Requantization of the int32 output to int8, per output channel k:
+ *   y = clamp(zero_point + round(acc * mult[k] / 2^shift[k]), -128, 127)
+ * with shift[k] clamped to [0, 62], the product exact in int64 (|acc| and
+ * |mult| are at most 2^31, so |p| <= 2^62), and round() rounding ties away
+ * from zero.  The lab's own definition (the reference has no requantizing
+ * code; its cuDNN comparison writes INT8 output, README.md:89-90).  Parity
+ * is pinned by an exact rational computation in tests/test_requant.py.
+ * acc and out are [pixels][channels] (NHWK).
+ */
+static int64_t requant_round(int64_t p, int s) {
+  if (s == 0) return p;
+  const int64_t half = (int64_t)1 << (s - 1);
+  return p >= 0 ? (p + half) >> s : -((-p + half) >> s);
+}
+
+void oracle_requantize(const int32_t *acc, int64_t pixels, int32_t channels,
+                       const int32_t *mult, const int32_t *shift, int32_t zero_point,
+                       int8_t *out) {
+  for (int64_t m = 0; m < pixels; ++m) {
+    for (int32_t k = 0; k < channels; ++k) {
+      const int s = shift[k] < 0 ? 0 : (shift[k] > 62 ? 62 : shift[k]);
+      const int64_t p = (int64_t)acc[m * channels + k] * (int64_t)mult[k];
+      int64_t q = requant_round(p, s) + (int64_t)zero_point;
+      if (q < -128) q = -128;
+      if (q > 127) q = 127;
+      out[m * channels + k] = (int8_t)q;
+    }
+  }
 }

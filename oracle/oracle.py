@@ -48,6 +48,9 @@ def lib():
         h.oracle_validate_sampled.argtypes = [POINTER(OShape), c_void_p, c_void_p, c_void_p, c_void_p]
         h.oracle_strip_eligible_reference.restype = c_int
         h.oracle_strip_eligible_reference.argtypes = [POINTER(OShape)]
+        h.oracle_requantize.restype = None
+        h.oracle_requantize.argtypes = [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
+                                        c_void_p]
         _lib = h
     return _lib
 
@@ -99,3 +102,16 @@ def validate_sampled(shape, x, w, b, output) -> int:
 def strip_eligible_reference(shape) -> bool:
     """spatial_strip.cuh:11-15 (the reference's predicate, not the gfx950 one)."""
     return bool(lib().oracle_strip_eligible_reference(ctypes.byref(_shape(shape))))
+
+
+def requantize(acc, mult, shift, zero_point: int) -> np.ndarray:
+    """The lab's int32 -> int8 requantization (no reference code; see
+    conv_oracle.c): acc [..., K] int32, mult/shift [K] int32 -> int8."""
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    k = acc.shape[-1]
+    mult = np.ascontiguousarray(mult, dtype=np.int32).reshape(k)
+    shift = np.ascontiguousarray(shift, dtype=np.int32).reshape(k)
+    out = np.empty(acc.shape, dtype=np.int8)
+    lib().oracle_requantize(acc.ctypes.data, int(acc.size // k), int(k), mult.ctypes.data,
+                            shift.ctypes.data, int(zero_point), out.ctypes.data)
+    return out

@@ -1,0 +1,247 @@
+"""The int32 -> int8 requantization: the oracle pinned by exact rational
+arithmetic (CPU), and the GPU paths (standalone kernel, fused epilogue,
+dispatched conv + requant) bit-exact against the oracle.
+
+The reference has no requantizing code (its cuDNN comparison writes INT8,
+README.md:89-90); the lab defines
+    y = clamp(zero_point + round(acc * mult[k] / 2^shift[k]), -128, 127)
+with shift clamped to [0, 62] and ties rounded away from zero.  The checks
+below compute that from its definition with Python's exact Fractions, not
+by repeating the oracle's shift-and-add steps.
+"""
+from fractions import Fraction
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+
+def exact_requant(acc: int, mult: int, shift: int, zp: int) -> int:
+    s = min(max(shift, 0), 62)
+    x = Fraction(acc * mult, 2 ** s)
+    mag = math.floor(abs(x) + Fraction(1, 2))  # ties away from zero
+    r = mag if x >= 0 else -mag
+    return max(-128, min(127, r + zp))
+
+
+def _check(acc, mult, shift, zp):
+    got = oracle.requantize(acc, mult, shift, zp)
+    k = acc.shape[-1]
+    flat = acc.reshape(-1, k)
+    exp = np.array([[exact_requant(int(a), int(mult[j]), int(shift[j]), zp)
+                     for j, a in enumerate(row)] for row in flat], dtype=np.int8).reshape(acc.shape)
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_requant_oracle_matches_exact_rationals_random():
+    rng = np.random.default_rng(7)
+    k = 13
+    acc = rng.integers(-(2 ** 31), 2 ** 31, size=(40, k), dtype=np.int64).astype(np.int32)
+    acc[0, :] = np.iinfo(np.int32).min
+    acc[1, :] = np.iinfo(np.int32).max
+    mult = rng.integers(-(2 ** 31), 2 ** 31, size=k, dtype=np.int64).astype(np.int32)
+    mult[0] = np.iinfo(np.int32).min
+    mult[1] = np.iinfo(np.int32).max
+    shift = rng.integers(0, 63, size=k).astype(np.int32)
+    shift[2], shift[3] = 0, 62
+    for zp in (0, -128, 5, 127):
+        _check(acc, mult, shift, zp)
+
+
+def test_requant_oracle_typical_scales():
+    # the usual case: a positive Q31 multiplier in [2^30, 2^31) and shifts
+    # that bring accumulators of a few million into int8 range
+    rng = np.random.default_rng(11)
+    k = 8
+    acc = rng.integers(-(2 ** 24), 2 ** 24, size=(200, k)).astype(np.int32)
+    mult = rng.integers(2 ** 30, 2 ** 31, size=k).astype(np.int32)
+    shift = rng.integers(40, 56, size=k).astype(np.int32)
+    _check(acc, mult, shift, 3)
+
+
+def test_requant_oracle_special_cases():
+    acc = np.array([[-300, -129, -128, -1, 0, 1, 127, 128, 300]], dtype=np.int32)
+    k = acc.shape[1]
+    one = np.ones(k, dtype=np.int32)
+    zero = np.zeros(k, dtype=np.int32)
+    # mult 1, shift 0: saturation of acc + zp
+    np.testing.assert_array_equal(oracle.requantize(acc, one, zero, 0)[0],
+                                  [-128, -128, -128, -1, 0, 1, 127, 127, 127])
+    np.testing.assert_array_equal(oracle.requantize(acc, one, zero, 10)[0],
+                                  [-128, -119, -118, 9, 10, 11, 127, 127, 127])
+    # mult 2^s with shift s is the identity before saturation
+    for s in (1, 7, 30):
+        np.testing.assert_array_equal(oracle.requantize(acc, one * (1 << s) if s < 31 else one,
+                                                        one * s, 0),
+                                      oracle.requantize(acc, one, zero, 0))
+    # halves round away from zero: acc * 1 / 2
+    halves = np.array([[-5, -3, -1, 1, 3, 5, -4, 4]], dtype=np.int32)
+    h1 = np.ones(halves.shape[1], dtype=np.int32)
+    np.testing.assert_array_equal(oracle.requantize(halves, h1, h1, 0)[0],
+                                  [-3, -2, -1, 1, 2, 3, -2, 2])
+    # shift outside [0, 62] is clamped
+    np.testing.assert_array_equal(oracle.requantize(acc, one, zero - 5, 0),
+                                  oracle.requantize(acc, one, zero, 0))
+    big = np.full(k, 2 ** 31 - 1, dtype=np.int32)
+    np.testing.assert_array_equal(oracle.requantize(acc, big, zero + 100, 0),
+                                  oracle.requantize(acc, big, zero + 62, 0))
+
+
+def test_requant_oracle_detects_planted_rounding_error():
+    # a floor instead of ties-away rounding differs from the exact result
+    acc = np.array([[3]], dtype=np.int32)
+    assert exact_requant(3, 1, 1, 0) == 2
+    assert int(oracle.requantize(acc, np.array([1], np.int32), np.array([1], np.int32), 0)[0, 0]) == 2
+    assert (3 * 1) >> 1 == 1  # the floor a plausible mistake would give
+
+
+# ---- ABI (no GPU) -----------------------------------------------------------
+
+import int8_kernel_lab_amd as lab
+from int8_kernel_lab_amd import _lib
+
+
+def _baseline(name):
+    import os
+    return lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), name)
+
+
+def test_requant_fused_only_for_the_row_kernel_with_copy_waves():
+    assert lab.requant_fused(_baseline("cfg2_resnet_3x3_s1"))
+    for name in ("cfg1_smoke", "cfg3_down_3x3_s2", "cfg4a_pointwise_1x1", "cfg5a_deep_k"):
+        assert not lab.requant_fused(_baseline(name))
+
+
+def test_requant_workspace_sizes():
+    s2 = _baseline("cfg2_resnet_3x3_s1")
+    assert lab.requant_workspace_bytes(s2) == 0
+    s3 = _baseline("cfg3_down_3x3_s2")
+    assert lab.requant_workspace_bytes(s3) == s3.output_elements * 4  # already 256-aligned
+    s5 = _baseline("cfg5a_deep_k")
+    acc = (s5.output_elements * 4 + 255) // 256 * 256
+    assert lab.requant_workspace_bytes(s5) == acc + lab.workspace_bytes("splitk", s5)
+
+
+def test_requant_launch_errors_without_gpu():
+    s3 = _baseline("cfg3_down_3x3_s2")
+    fake = 1 << 20  # never dereferenced: the checks fail before any launch
+    with pytest.raises(lab.I8ConvError) as e:
+        lab.launch_requant(s3, fake, fake, fake, fake, fake, 0, fake, None, 0)
+    assert e.value.status == _lib.WORKSPACE_TOO_SMALL
+    with pytest.raises(lab.I8ConvError) as e:
+        lab.launch_requant(s3, fake, fake, fake, None, fake, 0, fake, fake, 1 << 30)
+    assert e.value.status == _lib.BAD_ARGUMENT
+    with pytest.raises(lab.I8ConvError) as e:
+        lab.requantize(fake, 10, 0, fake, fake, 0, fake)
+    assert e.value.status == _lib.BAD_ARGUMENT
+
+
+# ---- GPU: bit-exact against the oracle --------------------------------------
+
+def _qparams(k, seed=3):
+    """Per-channel parameters that map accumulators of about 2^28 onto int8,
+    plus a few saturating and exactly-representable channels."""
+    rng = np.random.default_rng(seed)
+    mult = rng.integers(2 ** 30, 2 ** 31, size=k).astype(np.int32)
+    shift = rng.integers(50, 54, size=k).astype(np.int32)
+    if k > 4:
+        mult[0], shift[0] = 1, 0            # saturates nearly everything
+        mult[1], shift[1] = -(2 ** 31), 58  # negative multiplier
+        mult[2], shift[2] = 1 << 20, 20     # identity before saturation
+        mult[3], shift[3] = 3, 62           # everything rounds to 0
+    return mult, shift
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("channels", [64, 6])
+def test_requantize_kernel_bit_exact(channels):
+    from tests.conftest import say
+    rng = np.random.default_rng(channels)
+    pixels = 4099
+    acc = rng.integers(-(2 ** 31), 2 ** 31, size=(pixels, channels), dtype=np.int64).astype(np.int32)
+    mult, shift = _qparams(channels)
+    say(f"[gpu] requantize {pixels}x{channels}")
+    bufs = [lab.DeviceBuffer.from_array(a) for a in (acc, mult, shift)]
+    out = lab.DeviceBuffer(pixels * channels)
+    out.fill(0x5A)
+    lab.requantize(bufs[0], pixels, channels, bufs[1], bufs[2], -7, out)
+    lab.synchronize()
+    got = out.download(np.int8, pixels * channels).reshape(pixels, channels)
+    np.testing.assert_array_equal(got, oracle.requantize(acc, mult, shift, -7))
+
+
+REQUANT_CASES = ["cfg1_smoke", "cfg2_resnet_3x3_s1", "cfg3_down_3x3_s2", "cfg4a_pointwise_1x1",
+                 "cfg4b_k36_tail", "cfg5a_deep_k", "cfg5b_dilated"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", REQUANT_CASES)
+def test_conv_requant_bit_exact_on_baseline_configs(name):
+    from tests.conftest import say
+    shape = _baseline(name)
+    x, w, b = lab.make_case_data(shape)
+    mult, shift = _qparams(shape.k)
+    say(f"[gpu] conv2d_requant {name} fused={lab.requant_fused(shape)}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, 3, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, 3)
+    np.testing.assert_array_equal(got, exp)
+
+
+FUSED_EDGES = {
+    # the row kernel with copy waves in its int8 form: channel tail (byte
+    # stores), one, two and four fragments per row, unequal blocks, no padding
+    "k126_tail": lab.ConvShape(4, 30, 30, 128, 126, 3, 3, 1, 1, 1, 1, 1, 1),
+    "nfr1": lab.ConvShape(8, 14, 14, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
+    "nfr4": lab.ConvShape(4, 20, 60, 128, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    "r2_uneven": lab.ConvShape(8, 28, 28, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
+    "pad0": lab.ConvShape(4, 30, 30, 128, 64, 3, 3, 0, 0, 1, 1, 1, 1),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(FUSED_EDGES))
+def test_fused_requant_edges_bit_exact(name):
+    from tests.conftest import say
+    shape = FUSED_EDGES[name]
+    assert lab.requant_fused(shape), name
+    x, w, b = lab.make_case_data(shape, seed=99)
+    mult, shift = _qparams(shape.k, seed=5)
+    say(f"[gpu] fused requant {name} {shape}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, -20, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, -20)
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_kernel_requant_function_matches_oracle_on_host(tmp_path):
+    # the device function itself, built for the host with g++
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    exe = tmp_path / "requant_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-I", os.path.join(root, "include"), "-I",
+                    os.path.join(root, "int8_kernel_lab_amd", "csrc"),
+                    os.path.join(root, "tests", "requant_check.cpp"), "-o", str(exe)], check=True)
+    rng = np.random.default_rng(21)
+    n = 4000
+    acc = rng.integers(-(2 ** 31), 2 ** 31, size=n, dtype=np.int64)
+    mult = rng.integers(-(2 ** 31), 2 ** 31, size=n, dtype=np.int64)
+    shift = rng.integers(-3, 66, size=n, dtype=np.int64)
+    zp = rng.integers(-200, 200, size=n, dtype=np.int64)
+    # edges: extremes, exact ties of both signs, shift 0 and 62
+    acc[:8] = [-(2 ** 31), 2 ** 31 - 1, 3, -3, 5, -5, 1, -1]
+    mult[:8] = [-(2 ** 31), -(2 ** 31), 1, 1, 1, 1, 2 ** 31 - 1, 2 ** 31 - 1]
+    shift[:8] = [62, 0, 1, 1, 1, 1, 62, 62]
+    zp[:8] = 0
+    # a block of typical Q31 scales
+    acc[8:400] = rng.integers(-(2 ** 26), 2 ** 26, size=392)
+    mult[8:400] = rng.integers(2 ** 30, 2 ** 31, size=392)
+    shift[8:400] = rng.integers(48, 58, size=392)
+    text = "\n".join(f"{a} {m} {s} {z}" for a, m, s, z in zip(acc, mult, shift, zp))
+    out = subprocess.run([str(exe)], input=text, text=True, capture_output=True, check=True)
+    got = np.array([int(v) for v in out.stdout.split()], dtype=np.int64)
+    assert got.size == n
+    for i in range(n):
+        want = exact_requant(int(acc[i]), int(mult[i]), int(shift[i]), int(zp[i]))
+        assert got[i] == want, (i, acc[i], mult[i], shift[i], zp[i], got[i], want)
