@@ -176,6 +176,28 @@ int i8conv_measure_requant(const i8conv_shape *shape, const int8_t *input,
                            size_t workspace_bytes, void *stream, int warmup,
                            int iterations, float *median_ms, float *batched_ms);
 
+/* ---- layout transforms (the step before and after the path) ------------ */
+
+/* Asynchronous on `stream`; no workspace; tensors below 2^31 bytes.
+ * NCHW -> NHWC int8 (activations in NCHW order into the kernels' layout). */
+int i8conv_nchw_to_nhwc(const int8_t *src, int8_t *dst, int n, int c, int h,
+                        int w, void *stream);
+/* NHWC -> NCHW int8. */
+int i8conv_nhwc_to_nchw(const int8_t *src, int8_t *dst, int n, int h, int w,
+                        int c, void *stream);
+/* NHWK -> NKHW int32 (the convolution's output in channel-major order). */
+int i8conv_nhwk_to_nkhw(const int32_t *src, int32_t *dst, int n, int h, int w,
+                        int k, void *stream);
+/* pack_x / pack_w of the reference's cuDNN comparison (src/cudnn_lab.cu:7-18)
+ * on the GPU: NHWC (or KRSC: n = k, h = r, w = s) -> N, C/vect, H, W, vect,
+ * p[(c % V) + V*(w + W*(h + H*(c/V + C/V*n)))] = x[((n*H + h)*W + w)*C + c];
+ * vect % 16 == 0 and c % vect == 0 (the reference uses vect = 32). */
+int i8conv_pack_vect_c(const int8_t *src, int8_t *dst, int n, int h, int w,
+                       int c, int vect, void *stream);
+/* The inverse of i8conv_pack_vect_c. */
+int i8conv_unpack_vect_c(const int8_t *src, int8_t *dst, int n, int h, int w,
+                         int c, int vect, void *stream);
+
 /* ---- thin HIP runtime layer used by the host driver -------------------- */
 
 /* DeviceBuffer (conv_lab.cu:24-37) as C calls. */

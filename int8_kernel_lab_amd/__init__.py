@@ -36,7 +36,8 @@ __all__ = [
     "make_case_data", "measure", "spatial_strip_eligible", "workspace_bytes",
     "WORKLOADS_DIR", "BASELINE_SEED", "device_count", "device_info", "set_device",
     "synchronize", "requantize", "requant_fused", "requant_workspace_bytes", "launch_requant",
-    "conv2d_requant", "measure_requant",
+    "conv2d_requant", "measure_requant", "nchw_to_nhwc", "nhwc_to_nchw", "nhwk_to_nkhw",
+    "pack_vect_c", "unpack_vect_c",
 ]
 
 KERNELS = ("generic", "strip", "halo", "splitk")
@@ -421,3 +422,31 @@ def measure_requant(shape: ConvShape, input, filter, bias, mult, shift, zero_poi
                                        _ptr(stream), int(warmup), int(iterations),
                                        ctypes.byref(med), ctypes.byref(bat)), "measure_requant")
     return med.value, bat.value
+
+
+# ---- layout transforms (the step before and after the path) ----------------
+
+def nchw_to_nhwc(src, dst, n: int, c: int, h: int, w: int, stream=None) -> None:
+    check(lib().i8conv_nchw_to_nhwc(_ptr(src), _ptr(dst), n, c, h, w, _ptr(stream)),
+          "nchw_to_nhwc")
+
+
+def nhwc_to_nchw(src, dst, n: int, h: int, w: int, c: int, stream=None) -> None:
+    check(lib().i8conv_nhwc_to_nchw(_ptr(src), _ptr(dst), n, h, w, c, _ptr(stream)),
+          "nhwc_to_nchw")
+
+
+def nhwk_to_nkhw(src, dst, n: int, h: int, w: int, k: int, stream=None) -> None:
+    check(lib().i8conv_nhwk_to_nkhw(_ptr(src), _ptr(dst), n, h, w, k, _ptr(stream)),
+          "nhwk_to_nkhw")
+
+
+def pack_vect_c(src, dst, n: int, h: int, w: int, c: int, vect: int = 32, stream=None) -> None:
+    """src/cudnn_lab.cu:7-18 (pack_x / pack_w) on the GPU."""
+    check(lib().i8conv_pack_vect_c(_ptr(src), _ptr(dst), n, h, w, c, vect, _ptr(stream)),
+          "pack_vect_c")
+
+
+def unpack_vect_c(src, dst, n: int, h: int, w: int, c: int, vect: int = 32, stream=None) -> None:
+    check(lib().i8conv_unpack_vect_c(_ptr(src), _ptr(dst), n, h, w, c, vect, _ptr(stream)),
+          "unpack_vect_c")

@@ -70,6 +70,13 @@ SIGNATURES = {
     "i8conv_measure_requant": (c_int, [POINTER(CShape), c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p,
                                        c_int, c_int, POINTER(c_float), POINTER(c_float)]),
+    "i8conv_nchw_to_nhwc": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "i8conv_nhwc_to_nchw": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "i8conv_nhwk_to_nkhw": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "i8conv_pack_vect_c": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                   c_void_p]),
+    "i8conv_unpack_vect_c": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                     c_void_p]),
     "i8conv_device_count": (c_int, [POINTER(c_int)]),
     "i8conv_set_device": (c_int, [c_int]),
     "i8conv_device_alloc": (c_int, [POINTER(c_void_p), c_size_t]),

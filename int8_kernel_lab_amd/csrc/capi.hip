@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <string>
 #include <vector>
 
@@ -371,6 +372,76 @@ int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input, const 
                               workspace_bytes - acc_bytes, stream);
   if (r != I8CONV_OK) return r;
   return launch_requant(acc, g.gemm_m, g.gemm_n, mult, shift, zero_point, output, stream);
+}
+
+// ---- layout transforms -------------------------------------------------------
+
+namespace {
+int check_layout(const void *src, const void *dst, int64_t elements, int esize,
+                 std::initializer_list<int> dims) {
+  for (int d : dims)
+    if (d < 0) {
+      set_error("layout: negative dimension");
+      return I8CONV_BAD_ARGUMENT;
+    }
+  if (elements * esize >= (int64_t(1) << 31)) {
+    set_error("layout: tensors must be below 2^31 bytes");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  if (elements > 0 && (!src || !dst || src == dst)) {
+    set_error("layout: null or aliasing tensor pointers");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  if (!aligned(src, esize) || !aligned(dst, esize)) {
+    set_error("layout: tensors must be aligned to their element size");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  return I8CONV_OK;
+}
+}  // namespace
+
+int i8conv_nchw_to_nhwc(const int8_t *src, int8_t *dst, int n, int c, int h, int w,
+                        void *stream) {
+  const int rc = check_layout(src, dst, int64_t(n) * c * h * w, 1, {n, c, h, w});
+  if (rc != I8CONV_OK) return rc;
+  return launch_transpose(src, dst, n, c, h * w, 1, stream);
+}
+
+int i8conv_nhwc_to_nchw(const int8_t *src, int8_t *dst, int n, int h, int w, int c,
+                        void *stream) {
+  const int rc = check_layout(src, dst, int64_t(n) * c * h * w, 1, {n, c, h, w});
+  if (rc != I8CONV_OK) return rc;
+  return launch_transpose(src, dst, n, h * w, c, 1, stream);
+}
+
+int i8conv_nhwk_to_nkhw(const int32_t *src, int32_t *dst, int n, int h, int w, int k,
+                        void *stream) {
+  const int rc = check_layout(src, dst, int64_t(n) * k * h * w, 4, {n, k, h, w});
+  if (rc != I8CONV_OK) return rc;
+  return launch_transpose(src, dst, n, h * w, k, 4, stream);
+}
+
+namespace {
+int pack_common(const int8_t *src, int8_t *dst, int n, int h, int w, int c, int vect,
+                bool unpack, void *stream) {
+  const int rc = check_layout(src, dst, int64_t(n) * c * h * w, 1, {n, h, w, c});
+  if (rc != I8CONV_OK) return rc;
+  if (vect <= 0 || vect % 16 != 0 || c % vect != 0 || !aligned(src, 16) || !aligned(dst, 16)) {
+    set_error("pack_vect_c needs vect % 16 == 0, c % vect == 0 and 16-byte aligned tensors");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  return launch_pack_vect(src, dst, n, h, w, c, vect, unpack, stream);
+}
+}  // namespace
+
+int i8conv_pack_vect_c(const int8_t *src, int8_t *dst, int n, int h, int w, int c, int vect,
+                       void *stream) {
+  return pack_common(src, dst, n, h, w, c, vect, false, stream);
+}
+
+int i8conv_unpack_vect_c(const int8_t *src, int8_t *dst, int n, int h, int w, int c, int vect,
+                         void *stream) {
+  return pack_common(src, dst, n, h, w, c, vect, true, stream);
 }
 
 // ---- runtime layer -------------------------------------------------------

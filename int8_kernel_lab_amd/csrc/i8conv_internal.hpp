@@ -96,6 +96,12 @@ struct RequantArgs {
 };
 int launch_requant(const int32_t *acc, int64_t pixels, int32_t channels, const int32_t *mult,
                    const int32_t *shift, int32_t zero_point, int8_t *out, void *stream);
+// kernel_layout.hip: batched [rows][cols] -> [cols][rows] of esize-byte
+// elements (1 or 4), and NHWC <-> N, C/vect, H, W, vect packing.
+int launch_transpose(const void *src, void *dst, int64_t batch, int rows, int cols, int esize,
+                     void *stream);
+int launch_pack_vect(const int8_t *src, int8_t *dst, int n, int h, int w, int c, int vect,
+                     bool unpack, void *stream);
 // q == nullptr: int32 output to a.y; else the requantized int8 output to
 // q->y, computed in the kernel's epilogue (a.y unused)
 int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream,

@@ -13,6 +13,11 @@
  *   oracle_conv              reference_value over every output index
  *   oracle_validate_sampled  src/conv_lab.cu:68-86 (sampling rule)
  *   oracle_strip_eligible_reference  include/spatial_strip.cuh:11-15
+ *   oracle_pack_vect_c       src/cudnn_lab.cu:7-18 (pack_x / pack_w: NHWC or
+ *                            KRSC -> channel vectors of `vect`, the layout
+ *                            of cuDNN's INT8x32 path) and its inverse
+ *   oracle_transpose         batched [rows][cols] -> [cols][rows] of 1- or
+ *                            4-byte elements (NCHW <-> NHWC, NHWK -> NKHW)
  *   oracle_requantize        the lab's int32 -> int8 requantization (no
  *                            reference code: the reference's vendor path
  *                            writes INT8, README.md:89-90; see below)
@@ -191,4 +196,36 @@ void oracle_requantize(const int32_t *acc, int64_t pixels, int32_t channels,
       out[m * channels + k] = (int8_t)q;
     }
   }
+}
+
+/*
+ * src/cudnn_lab.cu:7-18 (pack_x; pack_w is the same map over k, r, s, c):
+ *   p[(c % V) + V*(w + W*(h + H*(c / V + (C / V)*n)))] = x[((n*H + h)*W + w)*C + c]
+ * with V = vect (32 in the reference).  unpack != 0 applies the inverse.
+ */
+void oracle_pack_vect_c(const int8_t *src, int8_t *dst, int32_t n_, int32_t h_, int32_t w_,
+                        int32_t c_, int32_t vect, int unpack) {
+  const int64_t groups = c_ / vect;
+  for (int64_t n = 0; n < n_; ++n)
+    for (int64_t c = 0; c < c_; ++c)
+      for (int64_t h = 0; h < h_; ++h)
+        for (int64_t w = 0; w < w_; ++w) {
+          const int64_t packed = (c % vect) + vect * (w + w_ * (h + h_ * (c / vect + groups * n)));
+          const int64_t plain = ((n * h_ + h) * w_ + w) * c_ + c;
+          if (unpack) dst[plain] = src[packed];
+          else dst[packed] = src[plain];
+        }
+}
+
+/* Batched transpose: batch matrices of [rows][cols] elements of `esize`
+ * bytes (1 or 4) -> [cols][rows]. */
+void oracle_transpose(const void *src, void *dst, int64_t batch, int64_t rows, int64_t cols,
+                      int esize) {
+  const char *s = (const char *)src;
+  char *d = (char *)dst;
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t r = 0; r < rows; ++r)
+      for (int64_t c = 0; c < cols; ++c)
+        for (int e = 0; e < esize; ++e)
+          d[((b * cols + c) * rows + r) * esize + e] = s[((b * rows + r) * cols + c) * esize + e];
 }

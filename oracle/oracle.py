@@ -48,6 +48,11 @@ def lib():
         h.oracle_validate_sampled.argtypes = [POINTER(OShape), c_void_p, c_void_p, c_void_p, c_void_p]
         h.oracle_strip_eligible_reference.restype = c_int
         h.oracle_strip_eligible_reference.argtypes = [POINTER(OShape)]
+        h.oracle_pack_vect_c.restype = None
+        h.oracle_pack_vect_c.argtypes = [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                         c_int32, c_int]
+        h.oracle_transpose.restype = None
+        h.oracle_transpose.argtypes = [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int]
         h.oracle_requantize.restype = None
         h.oracle_requantize.argtypes = [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
                                         c_void_p]
@@ -115,3 +120,30 @@ def requantize(acc, mult, shift, zero_point: int) -> np.ndarray:
     lib().oracle_requantize(acc.ctypes.data, int(acc.size // k), int(k), mult.ctypes.data,
                             shift.ctypes.data, int(zero_point), out.ctypes.data)
     return out
+
+
+def pack_vect_c(x, vect: int = 32) -> np.ndarray:
+    """cudnn_lab.cu:7-18: NHWC (or KRSC) int8 -> N, C/vect, H, W, vect."""
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    n, h, w, c = x.shape
+    out = np.empty(n * h * w * c, dtype=np.int8)
+    lib().oracle_pack_vect_c(x.ctypes.data, out.ctypes.data, n, h, w, c, int(vect), 0)
+    return out.reshape(n, c // vect, h, w, vect)
+
+
+def unpack_vect_c(p, vect: int = 32) -> np.ndarray:
+    """The inverse of pack_vect_c: N, C/vect, H, W, vect -> NHWC."""
+    p = np.ascontiguousarray(p, dtype=np.int8)
+    n, g, h, w, v = p.shape
+    out = np.empty(p.size, dtype=np.int8)
+    lib().oracle_pack_vect_c(p.ctypes.data, out.ctypes.data, n, h, w, g * v, int(v), 1)
+    return out.reshape(n, h, w, g * v)
+
+
+def transpose(x, batch: int, rows: int, cols: int) -> np.ndarray:
+    """Batched [rows][cols] -> [cols][rows] of int8 or int32 elements."""
+    x = np.ascontiguousarray(x)
+    assert x.dtype in (np.int8, np.int32) and x.size == batch * rows * cols
+    out = np.empty(x.size, dtype=x.dtype)
+    lib().oracle_transpose(x.ctypes.data, out.ctypes.data, batch, rows, cols, x.dtype.itemsize)
+    return out.reshape(batch, cols, rows)
