@@ -152,8 +152,10 @@ def traffic_record(workload: str, kernel: str):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=100)
+    # the clocks settle after ~20 ms of back-to-back launches: 10000 warmup
+    # launches (~65 ms) before the 5000 timed ones (~33 ms)
+    ap.add_argument("--steps", type=int, default=5000)
+    ap.add_argument("--warmup", type=int, default=10000)
     ap.add_argument("--kernel", default="dispatch",
                     help="dispatch (default) or one of generic|strip|halo|splitk")
     ap.add_argument("--workload", default=WORKLOAD)

@@ -219,11 +219,12 @@ int i8conv_stream_destroy(void *stream);
 int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
                        size_t name_len);
 
-/* measure() (conv_lab.cu:88-110): `warmup` launches, synchronize, then
- * `iterations` launches each bracketed by its own event pair on `stream` and
- * synchronized; *median_ms is the median.  When batched_ms is non-NULL it
- * also times `iterations` back-to-back launches between one event pair and
- * stores the mean per launch (exposes per-launch event overhead). */
+/* measure() (conv_lab.cu:88-110): `warmup` launches, synchronize; when
+ * batched_ms is non-NULL, `iterations` back-to-back launches between one
+ * event pair on `stream` (mean per launch, right after the warmup); then
+ * `iterations` launches each bracketed by its own event pair and
+ * synchronized; *median_ms is their median (it includes per-launch event
+ * overhead). */
 int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
                    const int8_t *filter, const int32_t *bias, int32_t *output,
                    void *workspace, size_t workspace_bytes, void *stream,

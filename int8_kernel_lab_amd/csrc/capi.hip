@@ -25,9 +25,10 @@ bool aligned(const void *p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 // measure() of conv_lab.cu:88-110 around any launch: `warmup` launches,
-// synchronize, then `iterations` launches each bracketed by its own event
-// pair on `stream` and synchronized (median), plus `iterations` back-to-back
-// launches between one event pair (mean per launch).
+// then `iterations` back-to-back launches between one event pair on
+// `stream` (mean per launch: the timed steps follow the warmup directly),
+// then `iterations` launches each bracketed by its own event pair and
+// synchronized (median per launch).
 template <class Launch>
 int measure_loop(Launch launch, void *stream, int warmup, int iterations, float *median_ms,
                  float *batched_ms) {
@@ -49,6 +50,15 @@ int measure_loop(Launch launch, void *stream, int warmup, int iterations, float 
     return hip_fail("hipEventCreate", e);
   }
   int rc = I8CONV_OK;
+  if (batched_ms) {
+    float ms = 0.f;
+    if ((e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+    for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch();
+    if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+    if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
+    if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) rc = hip_fail("hipEventElapsedTime", e);
+    if (rc == I8CONV_OK) *batched_ms = ms / float(iterations);
+  }
   std::vector<float> samples;
   samples.reserve(size_t(iterations));
   for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) {
@@ -63,15 +73,6 @@ int measure_loop(Launch launch, void *stream, int warmup, int iterations, float 
   if (rc == I8CONV_OK) {
     std::sort(samples.begin(), samples.end());
     *median_ms = samples[samples.size() / 2];
-  }
-  if (rc == I8CONV_OK && batched_ms) {
-    float ms = 0.f;
-    if ((e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-    for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch();
-    if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-    if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
-    if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess) rc = hip_fail("hipEventElapsedTime", e);
-    if (rc == I8CONV_OK) *batched_ms = ms / float(iterations);
   }
   // teardown: a failure here cannot change the measured result
   (void)hipEventDestroy(start);
