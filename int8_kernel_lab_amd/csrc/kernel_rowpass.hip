@@ -103,10 +103,11 @@ __device__ __forceinline__ void flag_wait(uint32_t addr, int target) {
   }
 }
 
-// Per-MFMA-wave state of a row walk over NG channel groups at a time: NG ==
-// 1 walks the rows twice (group 0, then group 1; the two-pass form), NG == 2
-// once with both groups per row (the single-pass form).
-template <int R, int NFR, int NG, bool kQ>
+// State of one wave's row walk over output rows [OLO, OHI) of the block
+// (input rows OLO .. OHI + 1), NG channel groups at a time: NG == 1 walks
+// the rows twice (group 0, then group 1; the two-pass form), NG == 2 once
+// with both groups per row (the single-pass form).
+template <int R, int NFR, int NG, bool kQ, int OLO, int OHI>
 struct PassState {
   v4i wf[NG][kTaps];       // this wave's 16 channels, the walk's groups, all taps (t = fy*3 + fx)
   v4i acc[R][NFR];         // output rows of the block
@@ -130,11 +131,11 @@ struct PassState {
 
   static constexpr int mfmas_in_step(int ir) {
     int n = 0;
-    for (int fy = 0; fy < 3; ++fy) n += (ir - fy >= 0 && ir - fy < R) ? 1 : 0;
+    for (int fy = 0; fy < 3; ++fy) n += (ir - fy >= OLO && ir - fy < OHI) ? 1 : 0;
     return n * NG * 3 * NFR;
   }
   static constexpr int reads_in_step(int ir) {
-    return ir + 1 < R + 2 ? NG * 3 * NFR + (ir + 1 <= 2 ? NG * 3 : 0) : 0;
+    return ir + 1 < OHI + 2 ? NG * 3 * NFR + (ir + 1 - OLO <= 2 ? NG * 3 : 0) : 0;
   }
   // MFMAs and LDS reads (the next row's fragments and taps) of step ir.
   // Scheduling groups: MFMA m is preceded by the LDS reads that spread NR
@@ -181,12 +182,12 @@ struct PassState {
   }
 
   // Input row IR of the walk from group G: once the next row's chunk has
-  // landed, its fragments (and the next filter row's taps) are read,
+  // landed, its fragments (and, in the walk's first rows, the next filter
+  // row's taps: input row OLO + t first needs filter row t) are read,
   // interleaved with the MFMAs of this row into output rows IR - fy
   // (compile-time valid ones); in the last walk, output row IR - 3 is then
-  // stored.  The counter
-  // of the chunk after next is read here and checked one row later, so a
-  // chunk that has landed costs no wait.
+  // stored.  The counter of the chunk after next is read here and checked
+  // one row later, so a chunk that has landed costs no wait.
   template <int G, int IR>
   __device__ __forceinline__ void step(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                        int oc0, int lane) {
@@ -197,11 +198,12 @@ struct PassState {
       for (int fx = 0; fx < 3; ++fx)
 #pragma unroll
         for (int j = 0; j < NFR; ++j) cur[g][fx][j] = frag[g][fx][j];
-    if (IR + 1 < R + 2) {
+    if (IR + 1 < OHI + 2) {
       const int seen = peeked;
-      if (IR + 2 < R + 2) peeked = flag_peek(counter<G>(p, IR + 2));
+      if (IR + 2 < OHI + 2) peeked = flag_peek(counter<G>(p, IR + 2));
       if (seen < kCopyWaves) flag_wait(counter<G>(p, IR + 1), kCopyWaves);
-      if (IR + 1 <= 2) take_taps<G, (IR + 1 <= 2 ? IR + 1 : 0)>(lane);
+      constexpr int fy_next = IR + 1 - OLO;
+      if (fy_next <= 2) take_taps<G, (fy_next <= 2 ? fy_next : 0)>(lane);
       load_row<G>(p, IR + 1);
     }
 #pragma unroll
@@ -211,7 +213,7 @@ struct PassState {
 #pragma unroll
         for (int fy = 0; fy < 3; ++fy) {
           const int o = IR - fy;  // a constant once the loops are unrolled
-          if (o >= 0 && o < R) {
+          if (o >= OLO && o < OHI) {
 #pragma unroll
             for (int j = 0; j < NFR; ++j)
               acc[o][j] = mfma16(wf[g][fy * 3 + fx], cur[g][fx][j], acc[o][j]);
@@ -227,8 +229,8 @@ struct PassState {
     // row later, so that its accumulators are read long after the MFMAs that
     // wrote them (reading them right away would stall the wave until those
     // MFMAs drained, every row).
-    if (G + NG == kGroups && IR >= 3)
-      store_row<(IR >= 3 ? IR - 3 : 0)>(p, vec, rows_out, m_row0, oc0, lane);
+    if (G + NG == kGroups && IR >= OLO + 3)
+      store_row<(IR >= OLO + 3 ? IR - 3 : 0)>(p, vec, rows_out, m_row0, oc0, lane);
   }
 
   // Output row O: the accumulators already hold bias + dot products.  N % 4
@@ -281,23 +283,23 @@ struct PassState {
     }
   }
 
-  // The walk from group G over all R + 2 padded input rows.
+  // The walk from group G over padded input rows OLO .. OHI + 1.
   template <int G, size_t... I>
   __device__ __forceinline__ void walk(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                        int oc0, int lane, std::index_sequence<I...>) {
-    flag_wait(counter<G>(p, 0), kCopyWaves);
-    peeked = flag_peek(counter<G>(p, 1));
+    flag_wait(counter<G>(p, OLO), kCopyWaves);
+    peeked = flag_peek(counter<G>(p, OLO + 1));
     take_taps<G, 0>(lane);
-    load_row<G>(p, 0);
+    load_row<G>(p, OLO);
     if (G == 0) {
       // the accumulators start at the bias (the oracle adds the bias first)
       const v4i bv = *reinterpret_cast<const v4i *>(bias_lds + 16 * (lane >> 4));
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+      for (int r = OLO; r < OHI; ++r)
 #pragma unroll
         for (int j = 0; j < NFR; ++j) acc[r][j] = bv;
     }
-    (step<G, int(I)>(p, vec, rows_out, m_row0, oc0, lane), ...);
+    (step<G, OLO + int(I)>(p, vec, rows_out, m_row0, oc0, lane), ...);
   }
 };
 
@@ -368,106 +370,18 @@ struct CopySchedule {
   }
 };
 
-template <int R, int NFR, int NG, bool kQ>
-__global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
-  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-  const PassArgs p = p_arg;
-  pin_sgprs(p);
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool copier = wave_id >= 4;
-  // the MFMA wave this wave is (or copies the filter halves and bias for)
-  const int wave = wave_id & 3;
-
-  const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
-  const int tn = int(blockIdx.x) - rest * p.tiles_n;
-  const int b = int(fast_div(uint32_t(rest), p.div_blocks));
-  const int q = rest - b * p.blocks;
-  const int oy0 = int((int64_t(q) * p.out_h) / p.blocks);
-  const int rows_out = int((int64_t(q + 1) * p.out_h) / p.blocks) - oy0;  // <= R
-  const int tile_n = tn * 64;
-
-  // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows]
-  //      [filter halves: 18 KB per wave][chunk counters]
-  PassState<R, NFR, NG, kQ> st;
+// One wave's walk over output rows [OLO, OHI) of its block: output set-up,
+// then the walk(s) over the input rows, then the last row's store.
+template <int R, int NFR, int NG, bool kQ, int OLO, int OHI>
+__device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, int wave, int lane,
+                                         int b, int oy0, int rows_out, int tile_n) {
+  PassState<R, NFR, NG, kQ, OLO, OHI> st;
   st.bias_lds = smem + wave * 256;
   st.planes = smem + kHaloBiasLds;
   st.plane_bytes = p.plane_copies * 1024;
   const int8_t *ring = st.planes + kGroups * p.rows_in * st.plane_bytes;
   st.halves = ring + wave * kHalves * 1024;
   st.counters = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
-  const int nchunks = (kGroups / NG) * p.rows_in;
-
-  if (wave_id == 0 && lane < nchunks) {
-    // every counter starts at zero before any wave adds to it
-    asm volatile("ds_write_b32 %0, %1" ::"v"(st.counters + 4u * uint32_t(lane)), "v"(0)
-                 : "memory");
-  }
-  __syncthreads();
-
-  if (copier) {
-    const v4u xd = make_desc(p.x, p.x_bytes);
-    const v4u wd = make_desc(p.w, p.w_bytes);
-    const uint32_t planes_lds = lds_addr(st.planes);
-    // filter halves for MFMA wave `wave`: lane -> filter row 16*wave +
-    // lane/4 and 16-byte chunk lane%4, holding the chunk swz64 puts there
-    const int frow = lane >> 2;
-    const int fchunk = swz64_chunk(frow, lane & 3);
-    const int oc_copy = tile_n + wave * 16 + frow;
-    const uint32_t fbase = oc_copy < p.gemm_n
-                               ? uint32_t(oc_copy) * uint32_t(p.gemm_k) + uint32_t(16 * fchunk)
-                               : kOutOfRange;
-    const uint32_t halves_lds = lds_addr(st.halves);
-    // Chunk (groups g0 .. g0 + ng - 1, row r): the bias (first chunk), the
-    // filter taps of filter row r (r <= 2) and plane copies j = wave + 4i
-    // of padded input row r.  Copy j covers units [64j, 64j + 64) of the
-    // plane; unit u of pixel pix is slot pix*5 + u (u == 4: padding, left
-    // out of range -> zeros).
-    auto issue_chunk = [&](int g0, int r, int pw, int ng) {
-      if (g0 == 0 && r == 0) stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, st.bias_lds, lane);
-      for (int g = g0; g < g0 + ng; ++g) {
-        if (r <= 2) {
-#pragma unroll
-          for (int fx = 0; fx < 3; ++fx) {
-            const int t = 3 * r + fx;
-            lds_copy16(wd, halves_lds + uint32_t((g * kTaps + t) * 1024),
-                       fbase + uint32_t(t * 128 + g * 64));
-          }
-        }
-      }
-      const int vr = b * p.hp + oy0 + r;
-      const int bb = int(fast_div(uint32_t(vr), p.div_hp));
-      const int iy = vr - bb * p.hp - p.pad_h;
-      const bool row_ok = bb < p.n && unsigned(iy) < unsigned(p.h);
-      // modulo 2^32: exact wherever it is used (the sums below are in [0, 2^31))
-      const uint32_t row_off = uint32_t((bb * p.h + iy) * p.wd - p.pad_w) * uint32_t(p.c);
-      for (int g = g0; g < g0 + ng; ++g) {
-        for (int i = 0; i < pw; ++i) {
-          const int j = wave + 4 * i;
-          const int slot = j * 64 + lane;
-          const int pix = slot / kUnits;
-          const int u = slot - pix * kUnits;
-          const bool ok = row_ok && u < kUnits - 1 && unsigned(pix - p.pad_w) < unsigned(p.wd);
-          const uint32_t off = ok ? row_off + uint32_t(64 * g + pix * p.c + 16 * u) : kOutOfRange;
-          lds_copy16(xd, planes_lds + uint32_t((g * p.rows_in + r) * st.plane_bytes + j * 1024),
-                     off);
-        }
-      }
-    };
-    auto signal = [&](int c) {
-      if (lane == 0) flag_add(st.counters + 4u * uint32_t(c));
-    };
-    // plane copies per row and group this wave issues: j = wave, wave + 4
-    const int pw = p.plane_copies > wave ? (p.plane_copies - wave + 3) / 4 : 0;
-    if (pw == 0) CopySchedule<R, 0, NG>::run(issue_chunk, signal);
-    else if (pw == 1) CopySchedule<R, 1, NG>::run(issue_chunk, signal);
-    else CopySchedule<R, 2, NG>::run(issue_chunk, signal);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    return;
-  }
-
 #pragma unroll
   for (int fx = 0; fx < 3; ++fx)
 #pragma unroll
@@ -502,11 +416,134 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     }
   }
 
-  st.template walk<0>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
+  st.template walk<0>(p, vec, rows_out, m_row0, oc0, lane,
+                      std::make_index_sequence<OHI - OLO + 2>{});
   if constexpr (NG == 1)
-    st.template walk<1>(p, vec, rows_out, m_row0, oc0, lane, std::make_index_sequence<R + 2>{});
-  st.template store_row<R - 1>(p, vec, rows_out, m_row0, oc0, lane);
+    st.template walk<1>(p, vec, rows_out, m_row0, oc0, lane,
+                        std::make_index_sequence<OHI - OLO + 2>{});
+  st.template store_row<OHI - 1>(p, vec, rows_out, m_row0, oc0, lane);
 }
+
+// Output rows the MFMA waves walk when the copy waves take the rest of the
+// block once their copies have landed (0: the MFMA waves walk all R rows).
+// The copy waves are free from about the time the last input row lands, so
+// they take the block's last rows; the MFMA waves, which start after the
+// first chunk, take the first (R + 2) / 2.  Only the requantizing instances
+// split: their epilogue's VALU work per value is what a second walking wave
+// per SIMD hides (28x28x128, int8 output: 8.97 -> 8.39 us per launch); with
+// int32 output the split measured 6.47-6.49 against 6.50-6.61 us, no gain.
+constexpr int split_rows(int R, int NG, bool kQ) {
+  return kQ && NG == 2 && R >= 4 ? (R + 2) / 2 : 0;
+}
+
+template <int R, int NFR, int NG, bool kQ>
+__global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  const PassArgs p = p_arg;
+  pin_sgprs(p);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool copier = wave_id >= 4;
+  // the MFMA wave this wave is (or copies the filter halves and bias for)
+  const int wave = wave_id & 3;
+
+  const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
+  const int tn = int(blockIdx.x) - rest * p.tiles_n;
+  const int b = int(fast_div(uint32_t(rest), p.div_blocks));
+  const int q = rest - b * p.blocks;
+  const int oy0 = int((int64_t(q) * p.out_h) / p.blocks);
+  const int rows_out = int((int64_t(q + 1) * p.out_h) / p.blocks) - oy0;  // <= R
+  const int tile_n = tn * 64;
+
+  // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows]
+  //      [filter halves: 18 KB per wave][chunk counters]
+  const int8_t *bias_lds = smem + wave * 256;
+  const int8_t *planes = smem + kHaloBiasLds;
+  const int plane_bytes = p.plane_copies * 1024;
+  const int8_t *ring = planes + kGroups * p.rows_in * plane_bytes;
+  const int8_t *halves = ring + wave * kHalves * 1024;
+  const uint32_t counters = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
+  const int nchunks = (kGroups / NG) * p.rows_in;
+  constexpr int kSplit = split_rows(R, NG, kQ);
+
+  if (wave_id == 0 && lane < nchunks) {
+    // every counter starts at zero before any wave adds to it
+    asm volatile("ds_write_b32 %0, %1" ::"v"(counters + 4u * uint32_t(lane)), "v"(0)
+                 : "memory");
+  }
+  __syncthreads();
+
+  if (copier) {
+    const v4u xd = make_desc(p.x, p.x_bytes);
+    const v4u wd = make_desc(p.w, p.w_bytes);
+    const uint32_t planes_lds = lds_addr(planes);
+    // filter halves for MFMA wave `wave`: lane -> filter row 16*wave +
+    // lane/4 and 16-byte chunk lane%4, holding the chunk swz64 puts there
+    const int frow = lane >> 2;
+    const int fchunk = swz64_chunk(frow, lane & 3);
+    const int oc_copy = tile_n + wave * 16 + frow;
+    const uint32_t fbase = oc_copy < p.gemm_n
+                               ? uint32_t(oc_copy) * uint32_t(p.gemm_k) + uint32_t(16 * fchunk)
+                               : kOutOfRange;
+    const uint32_t halves_lds = lds_addr(halves);
+    // Chunk (groups g0 .. g0 + ng - 1, row r): the bias (first chunk), the
+    // filter taps of filter row r (r <= 2) and plane copies j = wave + 4i
+    // of padded input row r.  Copy j covers units [64j, 64j + 64) of the
+    // plane; unit u of pixel pix is slot pix*5 + u (u == 4: padding, left
+    // out of range -> zeros).
+    auto issue_chunk = [&](int g0, int r, int pw, int ng) {
+      if (g0 == 0 && r == 0) stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, bias_lds, lane);
+      for (int g = g0; g < g0 + ng; ++g) {
+        if (r <= 2) {
+#pragma unroll
+          for (int fx = 0; fx < 3; ++fx) {
+            const int t = 3 * r + fx;
+            lds_copy16(wd, halves_lds + uint32_t((g * kTaps + t) * 1024),
+                       fbase + uint32_t(t * 128 + g * 64));
+          }
+        }
+      }
+      const int vr = b * p.hp + oy0 + r;
+      const int bb = int(fast_div(uint32_t(vr), p.div_hp));
+      const int iy = vr - bb * p.hp - p.pad_h;
+      const bool row_ok = bb < p.n && unsigned(iy) < unsigned(p.h);
+      // modulo 2^32: exact wherever it is used (the sums below are in [0, 2^31))
+      const uint32_t row_off = uint32_t((bb * p.h + iy) * p.wd - p.pad_w) * uint32_t(p.c);
+      for (int g = g0; g < g0 + ng; ++g) {
+        for (int i = 0; i < pw; ++i) {
+          const int j = wave + 4 * i;
+          const int slot = j * 64 + lane;
+          const int pix = slot / kUnits;
+          const int u = slot - pix * kUnits;
+          const bool ok = row_ok && u < kUnits - 1 && unsigned(pix - p.pad_w) < unsigned(p.wd);
+          const uint32_t off = ok ? row_off + uint32_t(64 * g + pix * p.c + 16 * u) : kOutOfRange;
+          lds_copy16(xd, planes_lds + uint32_t((g * p.rows_in + r) * plane_bytes + j * 1024),
+                     off);
+        }
+      }
+    };
+    auto signal = [&](int c) {
+      if (lane == 0) flag_add(counters + 4u * uint32_t(c));
+    };
+    // plane copies per row and group this wave issues: j = wave, wave + 4
+    const int pw = p.plane_copies > wave ? (p.plane_copies - wave + 3) / 4 : 0;
+    if (pw == 0) CopySchedule<R, 0, NG>::run(issue_chunk, signal);
+    else if (pw == 1) CopySchedule<R, 1, NG>::run(issue_chunk, signal);
+    else CopySchedule<R, 2, NG>::run(issue_chunk, signal);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // With a split, the copy wave then walks the block's last rows for its
+    // MFMA wave's 16 channels (its copies have landed; the chunk counters
+    // say when the other copy waves' have).
+    if constexpr (kSplit > 0)
+      run_walk<R, NFR, NG, kQ, kSplit, R>(p, smem, wave, lane, b, oy0, rows_out, tile_n);
+    return;
+  }
+  run_walk<R, NFR, NG, kQ, 0, (kSplit > 0 ? kSplit : R)>(p, smem, wave, lane, b, oy0, rows_out,
+                                                          tile_n);
+}
+
 
 template <int R, int NFR, bool kQ>
 int launch_q(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
