@@ -102,6 +102,36 @@ I8_HD inline int32_t requant1(int32_t acc, int32_t mult, int32_t shift, int32_t 
   return int32_t(q < -128 ? -128 : (q > 127 ? 127 : q));
 }
 
+// Short form of requant1 for shift >= 33 and |zp| <= 2^30 (the usual Q31
+// scales), from per-channel constants am = |mult|, hh = 2^(s-33), sh = s - 32
+// (s = min(shift, 62)).  In sign-magnitude form round-half-away needs no tie
+// correction: with a = |acc|,
+//   round(|p| / 2^s) = floor((a*am + 2^(s-1)) / 2^s)
+//                    = (hi32(a*am) + hh) >> sh
+// because 2^(s-1) = hh * 2^32 adds nothing to the low word (no carry).  The
+// quotient is below 2^30 (a*am <= 2^62), so zp plus the signed quotient stays
+// inside int32; the sign is that of acc xor mult (a zero acc or mult gives a
+// zero quotient).  One 32-bit high multiply instead of a 64-bit product,
+// 64-bit add and shift.  Equal to requant1 wherever requant_short_ok holds.
+I8_HD inline bool requant_short_ok(int32_t shift) { return shift >= 33; }
+I8_HD inline bool requant_short_zp_ok(int32_t zp) { return zp >= -(1 << 30) && zp <= (1 << 30); }
+I8_HD inline uint32_t requant_short_am(int32_t mult) {
+  return mult < 0 ? 0u - uint32_t(mult) : uint32_t(mult);
+}
+// (1 for shifts the short form does not take, so that hh stays defined)
+I8_HD inline uint32_t requant_short_sh(int32_t shift) {
+  return shift < 33 ? 1u : uint32_t((shift > 62 ? 62 : shift) - 32);
+}
+I8_HD inline uint32_t requant_short_hh(int32_t shift) { return 1u << (requant_short_sh(shift) - 1); }
+I8_HD inline int32_t requant1_short(int32_t acc, uint32_t am, int32_t mult, uint32_t hh,
+                                    uint32_t sh, int32_t zp) {
+  const uint32_t a = acc < 0 ? 0u - uint32_t(acc) : uint32_t(acc);
+  const uint32_t r = (uint32_t((uint64_t(a) * am) >> 32) + hh) >> sh;
+  const uint32_t sg = uint32_t((acc ^ mult) >> 31);
+  const int32_t v = int32_t((r ^ sg) - sg) + zp;
+  return v < -128 ? -128 : (v > 127 ? 127 : v);
+}
+
 #if defined(__HIPCC__)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -235,6 +265,20 @@ __device__ __forceinline__ uint32_t requant4(v4i acc, v4i mult, v4i shift, int32
   for (int e = 0; e < 4; ++e)
     packed |= (uint32_t(requant1(acc[e], mult[e], shift[e], zp)) & 0xffu) << (8 * e);
   return packed;
+}
+
+// requant4 through requant1_short (am, hh, sh from requant_short_*); the
+// low bytes are gathered with two byte permutes: v_perm_b32 selector bytes
+// 0-3 pick from its second operand, 4-7 from its first, 0x0c gives zero.
+__device__ __forceinline__ uint32_t requant4_short(v4i acc, v4i am, v4i mult, v4i hh, v4i sh,
+                                                   int32_t zp) {
+  int32_t y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    y[e] = requant1_short(acc[e], uint32_t(am[e]), mult[e], uint32_t(hh[e]), uint32_t(sh[e]), zp);
+  const uint32_t lo = __builtin_amdgcn_perm(uint32_t(y[1]), uint32_t(y[0]), 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(uint32_t(y[3]), uint32_t(y[2]), 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // D = A x B + C over int8 -> int32.  A is 16 rows (lane % 16) by 64 k,

@@ -126,8 +126,12 @@ struct PassState {
   __amdgpu_buffer_rsrc_t yr;
   uint32_t voff[NFR];
   uint32_t row_stride;
-  // kQ: this lane's four channels' multiplier and shift
+  // kQ: this lane's four channels' multiplier and shift; |multiplier|,
+  // 2^(shift - 33) and shift - 32 for requant4_short, which the wave takes
+  // when all its channels have shift >= 33 and |zero point| <= 2^30 (qshort)
   v4i qm, qs;
+  v4i qam, qhh, qsh;
+  bool qshort;
 
   static constexpr int mfmas_in_step(int ir) {
     int n = 0;
@@ -246,10 +250,19 @@ struct PassState {
     if (O >= rows_out) return;
     if constexpr (kQ) {
       if (vec) {
+        // qshort is uniform over the wave: a scalar branch
+        if (qshort) {
 #pragma unroll
-        for (int j = 0; j < NFR; ++j)
-          __builtin_amdgcn_raw_buffer_store_b32(requant4(acc[O][j], qm, qs, p.qzp), yr, voff[j],
-                                                O * row_stride, kStoreStream);
+          for (int j = 0; j < NFR; ++j)
+            __builtin_amdgcn_raw_buffer_store_b32(
+                requant4_short(acc[O][j], qam, qm, qhh, qsh, p.qzp), yr, voff[j], O * row_stride,
+                kStoreStream);
+        } else {
+#pragma unroll
+          for (int j = 0; j < NFR; ++j)
+            __builtin_amdgcn_raw_buffer_store_b32(requant4(acc[O][j], qm, qs, p.qzp), yr, voff[j],
+                                                  O * row_stride, kStoreStream);
+        }
         return;
       }
       const int m_row = m_row0 + O * p.out_w;
@@ -414,6 +427,16 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
       st.qm[e] = __builtin_amdgcn_raw_buffer_load_b32(mr, uint32_t(oc0 + e) * 4u, 0, 0);
       st.qs[e] = __builtin_amdgcn_raw_buffer_load_b32(sr, uint32_t(oc0 + e) * 4u, 0, 0);
     }
+    bool ok = requant_short_zp_ok(p.qzp);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // channels past N are never stored: they do not hold the wave back
+      ok = ok && (oc0 + e >= p.gemm_n || requant_short_ok(st.qs[e]));
+      st.qam[e] = int32_t(requant_short_am(st.qm[e]));
+      st.qhh[e] = int32_t(requant_short_hh(st.qs[e]));
+      st.qsh[e] = int32_t(requant_short_sh(st.qs[e]));
+    }
+    st.qshort = __builtin_amdgcn_ballot_w64(!ok) == 0;
   }
 
   st.template walk<0>(p, vec, rows_out, m_row0, oc0, lane,

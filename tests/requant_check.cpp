@@ -1,7 +1,9 @@
-// Host build of the kernels' requantization (requant1 in i8conv_device.hpp),
-// driven by tests/test_requant.py: reads "acc mult shift zp" lines on stdin
-// and prints one result per line, which the test compares with the CPU
-// checker's restatement and with exact rational arithmetic.
+// Host build of the kernels' requantization (requant1 and requant1_short in
+// i8conv_device.hpp), driven by tests/test_requant.py: reads "acc mult shift
+// zp" lines on stdin and prints, per line, requant1's result and the short
+// form's (or requant1's again where the short form does not apply), which
+// the test compares with the CPU checker's restatement and with exact
+// rational arithmetic.
 #include <stdint.h>
 #include <stdio.h>
 
@@ -9,7 +11,15 @@
 
 int main() {
   long long acc, mult, shift, zp;
-  while (scanf("%lld %lld %lld %lld", &acc, &mult, &shift, &zp) == 4)
-    printf("%d\n", i8conv::requant1(int32_t(acc), int32_t(mult), int32_t(shift), int32_t(zp)));
+  while (scanf("%lld %lld %lld %lld", &acc, &mult, &shift, &zp) == 4) {
+    const int32_t a = int32_t(acc), m = int32_t(mult), s = int32_t(shift), z = int32_t(zp);
+    const int32_t full = i8conv::requant1(a, m, s, z);
+    const int32_t brief =
+        i8conv::requant_short_ok(s) && i8conv::requant_short_zp_ok(z)
+            ? i8conv::requant1_short(a, i8conv::requant_short_am(m), m, i8conv::requant_short_hh(s),
+                                     i8conv::requant_short_sh(s), z)
+            : full;
+    printf("%d %d\n", full, brief);
+  }
   return 0;
 }

@@ -217,6 +217,43 @@ def test_fused_requant_edges_bit_exact(name):
     np.testing.assert_array_equal(got, exp)
 
 
+SHORT_FORM = {
+    # every wave takes the short form (shift >= 33, |zp| <= 2^30) with
+    # multipliers of both signs; quotients spread over the int8 range
+    "short": (-3, ()),
+    # two waves' channels leave its domain (shift 32 and 20): those waves
+    # take the general form, the rest the short one
+    "mixed": (-3, ((77, 32), (5, 20))),
+    # zero point at the short form's limit
+    "zp_limit": (-(2 ** 30), ()),
+    # zero point just outside it: every wave takes the general form
+    "zp_outside": (2 ** 30 + 1, ()),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", sorted(SHORT_FORM))
+def test_fused_requant_short_form_bit_exact(variant):
+    from tests.conftest import say
+    shape = _baseline("cfg2_resnet_3x3_s1")
+    assert lab.requant_fused(shape)
+    x, w, b = lab.make_case_data(shape, seed=7)
+    rng = np.random.default_rng(8)
+    mult = (rng.integers(2 ** 30, 2 ** 31, size=shape.k)
+            * rng.choice([-1, 1], size=shape.k)).astype(np.int32)
+    mult[9] = -(2 ** 31)
+    shift = rng.integers(44, 47, size=shape.k).astype(np.int32)
+    zp, general = SHORT_FORM[variant]
+    for ch, sh in general:
+        shift[ch] = sh
+    say(f"[gpu] fused requant short form {variant}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, zp, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, zp)
+    if variant in ("short", "mixed"):
+        assert len(np.unique(exp)) > 200       # the quotients reach most int8 values
+    np.testing.assert_array_equal(got, exp)
+
+
 def test_kernel_requant_function_matches_oracle_on_host(tmp_path):
     # the device function itself, built for the host with g++
     import os
@@ -241,10 +278,30 @@ def test_kernel_requant_function_matches_oracle_on_host(tmp_path):
     acc[8:400] = rng.integers(-(2 ** 26), 2 ** 26, size=392)
     mult[8:400] = rng.integers(2 ** 30, 2 ** 31, size=392)
     shift[8:400] = rng.integers(48, 58, size=392)
+    # the short form's domain (shift >= 33, |zp| <= 2^30): its edges, exact
+    # ties of both signs, the largest quotients, zero points at the limit
+    acc[400:416] = [-(2 ** 31), -(2 ** 31), 2 ** 31 - 1, 2 ** 31 - 1, 0, 0, 3, -3,
+                    2 ** 20, -(2 ** 20), 1, -1, 2 ** 31 - 1, -(2 ** 31), 12345, -12345]
+    mult[400:416] = [-(2 ** 31), 2 ** 31 - 1, -(2 ** 31), 2 ** 31 - 1, -(2 ** 31), 7,
+                     2 ** 31 - 1, 2 ** 31 - 1, 2 ** 13, 2 ** 13, 2 ** 31 - 1, -(2 ** 31), 5, 5,
+                     -1, -1]
+    shift[400:416] = [33, 62, 33, 34, 40, 33, 33, 33, 34, 34, 62, 62, 66, 33, 33, 33]
+    zp[400:416] = [2 ** 30, -(2 ** 30), 0, 5, -7, 0, 0, 0, 0, 0, 2 ** 30, -(2 ** 30), 1, 1, -1, 1]
+    # exact ties at shift 33 of both signs: acc * mult = -+(2q + 1) * 2^32
+    for i, q in zip(range(416, 424), [0, 1, 5, 100, 0, 1, 5, 100]):
+        sign = 1 if i < 420 else -1
+        acc[i], mult[i], shift[i], zp[i] = sign * 2 * (2 * q + 1), -(2 ** 31), 33, 0
+    acc[424:1400] = rng.integers(-(2 ** 31), 2 ** 31, size=976)
+    mult[424:1400] = rng.integers(-(2 ** 31), 2 ** 31, size=976)
+    shift[424:1400] = rng.integers(33, 70, size=976)
+    zp[424:1400] = rng.integers(-(2 ** 30), 2 ** 30 + 1, size=976)
     text = "\n".join(f"{a} {m} {s} {z}" for a, m, s, z in zip(acc, mult, shift, zp))
     out = subprocess.run([str(exe)], input=text, text=True, capture_output=True, check=True)
-    got = np.array([int(v) for v in out.stdout.split()], dtype=np.int64)
-    assert got.size == n
+    got = np.array([int(v) for v in out.stdout.split()], dtype=np.int64).reshape(-1, 2)
+    assert got.shape[0] == n
+    short = (shift >= 33) & (np.abs(zp) <= 2 ** 30)
+    assert short.sum() > 1000
     for i in range(n):
         want = exact_requant(int(acc[i]), int(mult[i]), int(shift[i]), int(zp[i]))
-        assert got[i] == want, (i, acc[i], mult[i], shift[i], zp[i], got[i], want)
+        assert got[i, 0] == want, (i, acc[i], mult[i], shift[i], zp[i], got[i], want)
+        assert got[i, 1] == want, ("short", i, acc[i], mult[i], shift[i], zp[i], got[i], want)
