@@ -144,8 +144,9 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
   if (id == I8CONV_KERNEL_GENERIC || id == I8CONV_KERNEL_SPLITK) {
     const GemmPlan p = id == I8CONV_KERNEL_GENERIC ? plan_generic(*shape, g) : plan_splitk(*shape, g);
     d = std::string(kNames[id]) + (p.dma ? " pipelined" : " register-staged") + " tile " +
-        std::to_string(p.bm) + "px x " +
-        std::to_string(p.bn) + "oc, grid " + tiles(g.gemm_m, p.bm) + "x" +
+        std::to_string(p.bm) + "px x " + std::to_string(p.bn) + "oc" +
+        (p.m_step > 0 && p.m_step < p.bm ? " (" + std::to_string(p.m_step) + "px stored)" : "") +
+        ", grid " + tiles(g.gemm_m, p.m_step > 0 ? p.m_step : p.bm) + "x" +
         tiles(g.gemm_n, p.bn) + (p.splits > 1 ? "x" + std::to_string(p.splits) + " splits" : "") +
         ", " + std::to_string(p.stages) + " k-stages" +
         (p.dma && gemm_dma_copy_waves(p) > 0 ? ", " + std::to_string(gemm_dma_copy_waves(p)) + " copy waves" : "");

@@ -84,6 +84,9 @@ struct ConvArgs {
   // split-K: stages [split * stages_per_split, ...) of 128 k-bytes each
   int stages_per_split;
   int splits;
+  // pipelined GEMM: pixel rows a tile stores (its tile height, or fewer:
+  // the tile's last rows then read as zeros and are not stored)
+  int m_step;
 };
 
 // The lab's int32 -> int8 requantization of one value:

@@ -28,6 +28,9 @@ struct GemmPlan {
   int splits = 1;            // > 1 only for split-K
   int stages = 0;            // ceil(gemm_k / 128)
   int stages_per_split = 0;
+  // pipelined kernel: pixel rows each tile stores (bm, or fewer to even out
+  // the last round of workgroups; the tile's remaining rows are zeros)
+  int m_step = 0;
   // c % 128 == 0: the LDS-DMA pipelined kernel (kernel_gemm_dma.hip), else
   // the register-staged one (kernel_gemm.hip)
   bool dma = false;
@@ -38,6 +41,7 @@ bool gemm_dma_tile_supported(int bm, int bn);
 // every wave copies and runs MFMAs)
 int gemm_dma_copy_waves(const GemmPlan &p);
 GemmPlan plan_generic(const i8conv_shape &s, const i8conv_geometry &g);
+int gemm_dma_step(int64_t gemm_m, int64_t tiles_n, int bm, int bn);
 GemmPlan plan_splitk(const i8conv_shape &s, const i8conv_geometry &g);
 size_t splitk_workspace_bytes(const i8conv_geometry &g, const GemmPlan &p);
 

@@ -87,7 +87,9 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
   int tile = int(blockIdx.x);
   if (tile < 8 * per_xcd) tile = (tile % 8) * per_xcd + tile / 8;
   const int tiles_n = (a.gemm_n + BN - 1) / BN;
-  const int tile_m = (tile / tiles_n) * BM;
+  const int tile_m = (tile / tiles_n) * a.m_step;
+  // pixel rows this tile stores; rows from m_end on read as zeros
+  const int m_end = min(a.gemm_m, tile_m + a.m_step);
   const int tile_n = (tile % tiles_n) * BN;
   const int stages = a.gemm_k / kStageBytes;
   int s_begin = 0, s_end = stages;
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
     const int r = 8 * (wave + NW * (CPA + j)) + (lane >> 3);  // >= BN
     const int lc = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1);
     const int m = tile_m + r - BN;
-    if (m < a.gemm_m) {
+    if (m < m_end) {
       const int b = int(fast_div(uint32_t(m), a.div_ohw));
       const int rem = m - b * a.out_h * a.out_w;
       const int oy = int(fast_div(uint32_t(rem), a.div_ow));
@@ -271,7 +273,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
   // Epilogue: lane holds channels oc0..oc0+3 of pixel px for each fragment.
   int32_t *out = a.y;
   if (kSplit) out = a.partial + size_t(blockIdx.y) * size_t(a.gemm_m) * size_t(a.gemm_n);
-  const OutWindow ow = out_window(out, a.gemm_m, a.gemm_n, tile_m, BM);
+  const OutWindow ow = out_window(out, a.gemm_m, a.gemm_n, tile_m, a.m_step);
   const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ow.ok;
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
-      if (px >= a.gemm_m) continue;
+      if (px >= m_end) continue;
       const v4i v = add_wrap(acc[i][j], bv);
       if (vec) {
         if (oc0 < a.gemm_n)
@@ -297,7 +299,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
 
 template <int BM, int BN, int WM, int WN, int NCW = 0>
 int launch_tile(const ConvArgs &a, int splits, hipStream_t stream) {
-  const int tiles = int(((int64_t(a.gemm_m) + BM - 1) / BM) * ((a.gemm_n + BN - 1) / BN));
+  const int tiles = int(((int64_t(a.gemm_m) + a.m_step - 1) / a.m_step) * ((a.gemm_n + BN - 1) / BN));
   const int stages = a.gemm_k / kStageBytes;
   const int ring = std::min(kRing, splits > 1 ? a.stages_per_split : stages);
   const size_t lds = size_t(ring) * size_t(BM + BN) * kStageBytes;
@@ -342,15 +344,18 @@ int gemm_dma_copy_waves(const GemmPlan &p) {
   return p.bm == 128 && p.bn == 128 && per_workgroup >= 4 ? 4 : 0;
 }
 
-int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stream) {
+int launch_gemm_dma(const ConvArgs &args, const GemmPlan &p, int splits, void *stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
+  ConvArgs a = args;
+  a.m_step = p.m_step > 0 ? p.m_step : p.bm;
   // the kernel's assumptions, checked on the host: whole 128-byte stages in
   // one tap, a stage range per split, a tile it was built for, and LDS rows
   // the ring can hold
   const int stages = a.gemm_k / kStageBytes;
   if (a.c % kStageBytes != 0 || a.gemm_k % kStageBytes != 0 || stages < 1 ||
       (splits > 1 && (a.stages_per_split < 1 || int64_t(splits - 1) * a.stages_per_split >= stages)) ||
-      !gemm_dma_tile_supported(p.bm, p.bn) ||
+      !gemm_dma_tile_supported(p.bm, p.bn) || a.m_step % 16 != 0 || a.m_step > p.bm ||
+      a.m_step < 16 ||
       size_t(kRing) * size_t(p.bm + p.bn) * kStageBytes > size_t(kLdsBudget)) {
     set_error("pipelined gemm plan out of range");
     return I8CONV_BAD_ARGUMENT;

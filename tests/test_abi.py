@@ -237,3 +237,17 @@ def test_python_layer_raises_on_bad_calls(baseline_cases):
         lab.eligible("cudnn", baseline_cases["cfg1_smoke"])
     with pytest.raises(lab.I8ConvError, match="ineligible"):
         lab.launch("strip", baseline_cases["cfg3_down_3x3_s2"], FAKE, FAKE, FAKE, FAKE)
+
+
+def test_pipelined_tile_step_evens_out_the_last_round(baseline_cases):
+    # 1568 tiles of 128 pixels leave 32 workgroups for a last round on 256
+    # compute units; tiles storing 112 rows give 1792 = 7 * 256.  Grids of
+    # one round (196 and 256 tiles) keep whole tiles.
+    d = lab.describe("generic", baseline_cases["cfg4a_pointwise_1x1"])
+    assert "(112px stored), grid 1792x1" in d, d
+    d = lab.describe("generic", baseline_cases["cfg3_down_3x3_s2"])
+    assert "stored" not in d and "grid 98x2" in d, d
+    d = lab.describe("generic", baseline_cases["cfg5b_dilated"])
+    assert "stored" not in d and "grid 128x2" in d, d
+    # split-K keeps whole tiles
+    assert "stored" not in lab.describe("splitk", baseline_cases["cfg5a_deep_k"])

@@ -58,6 +58,11 @@ EDGE = {
     "dma_256x128_tails": lab.ConvShape(4, 63, 99, 128, 134, 3, 3, 1, 1, 1, 1, 1, 1),
     "dma_1x1_k62_short": lab.ConvShape(16, 56, 55, 256, 62, 1, 1, 0, 0, 1, 1, 1, 1),
     "dma_256x64_tails": lab.ConvShape(16, 57, 55, 128, 62, 3, 3, 1, 1, 1, 1, 1, 1),
+    # tiles that store fewer pixel rows than they hold (the tile step, 80 of
+    # 128 on grids just over 256 tiles): a partial last tile, with vector
+    # stores and with element stores (K % 4)
+    "dma_step_k100_tail": lab.ConvShape(17, 45, 45, 128, 100, 3, 3, 1, 1, 1, 1, 1, 1),
+    "dma_step_1x1_k70": lab.ConvShape(17, 45, 45, 256, 70, 1, 1, 0, 0, 1, 1, 1, 1),
     # c == 128 3x3 stride 1: the row-streaming kernel with copy waves.
     # Blocks of unequal height (8/7 and 2/1 output rows), a channel tail with
     # scalar stores, four fragments per row (the two-walk form, 5 plane
