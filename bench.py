@@ -6,9 +6,13 @@ the layer the >=50%-of-peak target is quoted on), on one GPU.
 A step = one convolution of the whole layer (7.40 GOP) with input, filter,
 bias and output resident in HBM.  Before timing, the GPU output is checked
 bit-exact against the CPU oracle (the reference's check-before-time
-contract, conv_lab.cu:193-194).  Timing: W warmup launches, synchronize,
+contract, conv_lab.cu:193-194).  Timing: the K steps are launched as
+replays of a HIP graph of 100 launches (a serving loop's form: the host
+enqueues one graph per 100 convolutions): W warmup launches, synchronize,
 then exactly K back-to-back launches between one pair of HIP events on the
-launch stream (plus the reference's per-launch median, conv_lab.cu:88-110).
+graph's stream; the output is checked again after them.  Beside it: the same
+K launches enqueued one by one on a stream, and the reference's per-launch
+median (conv_lab.cu:88-110).
 
 Prints one JSON line.  --gpus N > 1 is not supported (one GPU per box).
 """
@@ -209,8 +213,17 @@ def main() -> int:
               file=sys.stderr)
         return 1
 
-    median_ms, mean_ms = lab.measure(kernel, shape, xb, wb, bb, yb, ws, ws_n,
-                                     warmup=args.warmup, iterations=args.steps)
+    median_ms, stream_ms = lab.measure(kernel, shape, xb, wb, bb, yb, ws, ws_n,
+                                       warmup=args.warmup, iterations=args.steps)
+    per_graph = 100 if args.steps % 100 == 0 else 1
+    yb.fill(0xA5)
+    mean_ms = lab.measure_graph(kernel, shape, xb, wb, bb, yb, ws, ws_n, warmup=args.warmup,
+                                iterations=args.steps, launches_per_graph=per_graph)
+    got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
+    if not np.array_equal(got, expected):
+        print(f"bench.py: {kernel} output after the graph replays differs from the oracle",
+              file=sys.stderr)
+        return 1
     ops = shape.ops()
     nbytes = shape.algorithmic_bytes()
     tops = ops / (mean_ms * 1e-3) / 1e12
@@ -241,6 +254,11 @@ def main() -> int:
             "algorithmic_bytes_per_step": nbytes,
             "pct_int8_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
             "per_launch_median_ms": round(median_ms, 6),
+            "timing": f"HIP graph of {per_graph} launches replayed; "
+                      f"{args.steps} launches enqueued one by one on a stream: "
+                      f"{stream_ms * 1e3:.3f} us per launch "
+                      f"({ops / (stream_ms * 1e-3) / 1e12:.1f} TOPS)",
+            "stream_ms_per_step": round(stream_ms, 6),
             "device": info["arch"],
             "compute_units": info["compute_units"],
             "parallelism": "single GPU",

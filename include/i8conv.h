@@ -219,6 +219,19 @@ int i8conv_stream_destroy(void *stream);
 int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
                        size_t name_len);
 
+/* No counterpart in the reference, which times launches one by one
+ * (conv_lab.cu:88-110).  Back-to-back launches replayed from a HIP graph:
+ * one launch on a stream of its own (default priority), then a graph of
+ * `launches_per_graph` i8conv_launch calls (kernel nodes only) captured on
+ * it; ceil(warmup / launches_per_graph) replays, synchronize, then
+ * iterations / launches_per_graph replays between one event pair.
+ * *mean_ms = elapsed / iterations.  iterations must be a positive multiple
+ * of launches_per_graph.  Synchronous; the output holds the last launch's. */
+int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
+                         const int8_t *filter, const int32_t *bias, int32_t *output,
+                         void *workspace, size_t workspace_bytes, int warmup,
+                         int iterations, int launches_per_graph, float *mean_ms);
+
 /* measure() (conv_lab.cu:88-110): `warmup` launches, synchronize; when
  * batched_ms is non-NULL, `iterations` back-to-back launches between one
  * event pair on `stream` (mean per launch, right after the warmup); then

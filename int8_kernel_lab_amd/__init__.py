@@ -302,6 +302,23 @@ def measure(name: str, shape: ConvShape, input, filter, bias, output, workspace=
     return med.value, bat.value
 
 
+def measure_graph(name: str, shape: ConvShape, input, filter, bias, output, workspace=None,
+                  workspace_nbytes: int = 0, warmup: int = 10000, iterations: int = 5000,
+                  launches_per_graph: int = 100) -> float:
+    """Mean ms per launch of `iterations` back-to-back launches replayed from
+    a HIP graph of `launches_per_graph` launches (i8conv_measure_graph)."""
+    if isinstance(workspace, DeviceBuffer) and not workspace_nbytes:
+        workspace_nbytes = workspace.nbytes
+    mean = ctypes.c_float()
+    status = lib().i8conv_measure_graph(_kernel_id(name), ctypes.byref(shape.c_struct()),
+                                        _ptr(input), _ptr(filter), _ptr(bias), _ptr(output),
+                                        _ptr(workspace), int(workspace_nbytes), int(warmup),
+                                        int(iterations), int(launches_per_graph),
+                                        ctypes.byref(mean))
+    check(status, f"measure_graph {name}")
+    return mean.value
+
+
 def device_info() -> Dict[str, object]:
     cus = ctypes.c_int()
     clk = ctypes.c_int()

@@ -88,6 +88,9 @@ SIGNATURES = {
     "i8conv_stream_create": (c_int, [POINTER(c_void_p)]),
     "i8conv_stream_destroy": (c_int, [c_void_p]),
     "i8conv_device_info": (c_int, [POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]),
+    "i8conv_measure_graph": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,
+                                     c_void_p, c_void_p, c_size_t, c_int, c_int, c_int,
+                                     POINTER(c_float)]),
     "i8conv_measure": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,
                                c_void_p, c_void_p, c_size_t, c_void_p, c_int, c_int,
                                POINTER(c_float), POINTER(c_float)]),

@@ -543,6 +543,66 @@ int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
       stream, warmup, iterations, median_ms, batched_ms);
 }
 
+int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
+                         const int8_t *filter, const int32_t *bias, int32_t *output,
+                         void *workspace, size_t workspace_bytes, int warmup, int iterations,
+                         int launches_per_graph, float *mean_ms) {
+  if (warmup < 0 || iterations <= 0 || launches_per_graph <= 0 || !mean_ms ||
+      iterations % launches_per_graph != 0) {
+    set_error("measure_graph needs warmup >= 0, iterations a positive multiple of "
+              "launches_per_graph, and an output");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail("hipStreamCreateWithFlags", e);
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipEvent_t start = nullptr, stop = nullptr;
+  auto launch = [&]() {
+    return i8conv_launch(id, shape, input, filter, bias, output, workspace, workspace_bytes, s);
+  };
+  // one launch outside the graph (checks the arguments, sets any function
+  // attribute the kernel needs), then the capture of launches_per_graph
+  // launches: kernel nodes only
+  int rc = launch();
+  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("launch", e);
+  if (rc == I8CONV_OK &&
+      (e = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed)) != hipSuccess)
+    rc = hip_fail("hipStreamBeginCapture", e);
+  if (rc == I8CONV_OK) {
+    for (int i = 0; i < launches_per_graph && rc == I8CONV_OK; ++i) rc = launch();
+    // end the capture whatever happened inside it
+    const hipError_t ec = hipStreamEndCapture(s, &graph);
+    if (rc == I8CONV_OK && ec != hipSuccess) rc = hip_fail("hipStreamEndCapture", ec);
+  }
+  if (rc == I8CONV_OK && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
+    rc = hip_fail("hipGraphInstantiate", e);
+  const int warm_replays = (warmup + launches_per_graph - 1) / launches_per_graph;
+  for (int i = 0; i < warm_replays && rc == I8CONV_OK; ++i)
+    if ((e = hipGraphLaunch(exec, s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
+  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("warmup", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&start)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&stop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  for (int i = 0; i < iterations / launches_per_graph && rc == I8CONV_OK; ++i)
+    if ((e = hipGraphLaunch(exec, s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
+  if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
+  float ms = 0.f;
+  if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess)
+    rc = hip_fail("hipEventElapsedTime", e);
+  if (rc == I8CONV_OK) *mean_ms = ms / float(iterations);
+  // teardown: drain the stream first; a failure here cannot change the result
+  (void)hipStreamSynchronize(s);
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+  (void)hipStreamDestroy(s);
+  return rc;
+}
+
 int i8conv_measure_requant(const i8conv_shape *shape, const int8_t *input, const int8_t *filter,
                            const int32_t *bias, const int32_t *mult, const int32_t *shift,
                            int32_t zero_point, int8_t *output, void *workspace,

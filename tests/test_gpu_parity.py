@@ -229,3 +229,32 @@ def test_launch_errors_are_statuses_not_faults(baseline_cases):
     finally:
         for buf in (xb, wb, bb, yb):
             buf.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["cfg2_resnet_3x3_s1", "cfg5a_deep_k"])
+def test_graph_replays_bit_exact(case, baseline_cases):
+    # the bench's timing path: launches captured in a HIP graph (split-K: two
+    # kernels per launch, the workspace rewritten every launch), replayed
+    # twice per call, two calls with the output poisoned and checked between
+    shape = baseline_cases[case]
+    kernel = lab.dispatch(shape)
+    x, w, b, expected = _case(case, shape)
+    g = shape.geometry()
+    bufs = [lab.DeviceBuffer.from_array(a) for a in (x, w, b)]
+    yb = lab.DeviceBuffer(4 * g.output_elements)
+    ws_n = lab.workspace_bytes(kernel, shape)
+    ws = lab.DeviceBuffer(ws_n) if ws_n else None
+    try:
+        for call in range(2):
+            say(f"[gpu] graph replays {kernel} on {case}, call {call}")
+            yb.fill(0x5A + call)
+            ms = lab.measure_graph(kernel, shape, *bufs, yb, ws, ws_n, warmup=2, iterations=6,
+                                   launches_per_graph=3)
+            assert ms > 0
+            got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
+            assert_bit_exact(got, expected, f"graph {kernel}/{case} call {call}")
+    finally:
+        for buf in bufs + [yb, ws]:
+            if buf is not None:
+                buf.close()
