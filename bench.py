@@ -6,13 +6,17 @@ the layer the >=50%-of-peak target is quoted on), on one GPU.
 A step = one convolution of the whole layer (7.40 GOP) with input, filter,
 bias and output resident in HBM.  Before timing, the GPU output is checked
 bit-exact against the CPU oracle (the reference's check-before-time
-contract, conv_lab.cu:193-194).  Timing: the K steps are launched as
-replays of a HIP graph of 100 launches (a serving loop's form: the host
-enqueues one graph per 100 convolutions): W warmup launches, synchronize,
-then exactly K back-to-back launches between one pair of HIP events on the
-graph's stream; the output is checked again after them.  Beside it: the same
-K launches enqueued one by one on a stream, and the reference's per-launch
-median (conv_lab.cu:88-110).
+contract, conv_lab.cu:193-194).  Timing (i8conv_measure_graph): the K steps
+are K back-to-back launches replayed from HIP graphs (a main graph of
+min(K, 100) launches, plus a graph of the K mod 100 left over), timed
+between one pair of HIP events on the graphs' stream, after a warmup of at
+least W launches AND at least --min-warmup-ms of wall time (back-to-back
+launches need some tens of ms to bring the clocks to their steady state).
+The output is poisoned right before the timed replays and checked against
+the oracle after them.  Beside it: the same K launches enqueued one by one
+on a stream, and the reference's per-launch median (conv_lab.cu:88-110).
+The CPU baseline is the C oracle (a port of conv_lab.cu:39-66) timed on
+this host, single-threaded and on all threads of the box's CPU share.
 
 Prints one JSON line.  --gpus N > 1 is not supported (one GPU per box).
 """
@@ -32,9 +36,31 @@ PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E, published
 WORKLOAD = "cfg2_resnet_3x3_s1"
 
 
-def cpu_baseline(shape, x, w, b, threads: int, min_cpu_seconds: float = 10.0):
-    """The oracle (a port of conv_lab.cu:39-66) on the host cores, repeated
-    over the full layer until about `min_cpu_seconds` of CPU work."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_threads() -> int:
+    """Threads of this process's CPU share: the CPUs it may run on, at most
+    16 (a one-GPU box's share of its host, whatever the host has)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def time_oracle(shape, x, w, b, threads: int, min_cpu_seconds: float, max_reps: int = 50):
+    """oracle.conv over the full layer on `threads` threads, repeated until
+    about `min_cpu_seconds` of CPU work (threads x wall); (TOPS, reps,
+    wall seconds)."""
     from oracle import oracle
     reps, t_total = 0, 0.0
     while True:
@@ -42,12 +68,32 @@ def cpu_baseline(shape, x, w, b, threads: int, min_cpu_seconds: float = 10.0):
         oracle.conv(shape, x, w, b, threads=threads)
         t_total += time.perf_counter() - t0
         reps += 1
-        if t_total * threads >= min_cpu_seconds or reps >= 50:
+        if t_total * threads >= min_cpu_seconds or reps >= max_reps:
             break
-    tops = shape.ops() * reps / t_total / 1e12
-    return {"value": round(tops, 6), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"oracle.conv over the full {WORKLOAD} layer x{reps} "
-                      f"({reps * shape.ops() / 1e9:.1f} GOP, {t_total:.2f} s wall)"}
+    return shape.ops() * reps / t_total / 1e12, reps, t_total
+
+
+def cpu_baseline(shape, x, w, b):
+    """The oracle (a port of conv_lab.cu:39-66: bias, then fy -> fx -> c per
+    output, int32) on this host's cores, in the same run as the GPU timing:
+    single-threaded (the reference's oracle is single-threaded) and on all
+    threads of the process's CPU share (`value`, `cores`).  Bounded samples
+    of the same workload: about 6 s of CPU work single-threaded and 12 s of
+    CPU work (threads x wall) on all threads."""
+    from oracle import oracle
+    threads = host_threads()
+    one, one_reps, one_s = time_oracle(shape, x, w, b, 1, 6.0)
+    many, many_reps, many_s = time_oracle(shape, x, w, b, threads, 12.0)
+    return {"value": round(many, 6), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"oracle.conv over the full {WORKLOAD} layer x{many_reps} on {threads} "
+                      f"threads ({many_reps * shape.ops() / 1e9:.1f} GOP, {many_s:.2f} s wall)",
+            "single_thread": {"value": round(one, 6), "unit": "TOPS", "cores": 1,
+                              "sample": f"the same layer x{one_reps} on 1 thread "
+                                        f"({one_reps * shape.ops() / 1e9:.1f} GOP, "
+                                        f"{one_s:.2f} s wall)"},
+            "hardware_concurrency": os.cpu_count(),
+            "cpu_model": cpu_model(),
+            "build": oracle.build_info()}
 
 
 def copy_calibration(mib: int, steps: int) -> int:
@@ -67,28 +113,41 @@ def copy_calibration(mib: int, steps: int) -> int:
     return 0
 
 
-def write_floor(workload: str, steps: int, warmup: int) -> int:
-    """Times torch's fill kernel over exactly the layer's output bytes (the
-    NHWK int32 tensor every candidate must store), back to back between two
-    events on the current stream: no convolution can finish faster."""
-    import torch
+def write_floor(workload: str, steps: int, warmup: int, min_warmup_ms: float) -> int:
+    """The store floor of the workload's dispatched row kernel: the lab's
+    store-only kernel (i8conv_measure_store_floor) writing exactly the
+    layer's int32 output bytes with the row kernel's 16-byte write-through
+    stores, in its launch shape (workgroups x 512 threads, the same dynamic
+    LDS), timed like the headline; beside it, an empty kernel of the same
+    shape (the dispatch floor) and ordinary stores."""
+    import numpy as np
     import int8_kernel_lab_amd as lab
     shape = lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), workload)
-    y = torch.empty(shape.geometry().output_elements, dtype=torch.int32, device="cuda")
-    for _ in range(warmup):
-        y.fill_(7)
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        y.fill_(7)
-    stop.record()
-    torch.cuda.synchronize()
-    us = start.elapsed_time(stop) * 1e3 / steps
-    print(json.dumps({"write_floor_workload": workload, "bytes": y.numel() * 4,
-                      "us_per_launch": round(us, 3),
-                      "tops_if_conv_took_this_long": round(shape.ops() / (us * 1e-6) / 1e12, 1),
-                      "launches": steps}), flush=True)
+    nbytes = 4 * shape.geometry().output_elements
+    plan = lab.describe(lab.dispatch(shape), shape)
+    grid = int(plan.split("grid ")[1].split()[0]) if "grid " in plan else 256
+    lds = int(plan.split("LDS ")[1].split()[0]) * 1024 if "copy waves" in plan else 0
+    y = lab.DeviceBuffer(nbytes)
+    out = {"write_floor_workload": workload, "bytes": nbytes, "workgroups": grid,
+           "threads": 512, "lds_bytes": lds, "launches": steps}
+    for key, n, through in (("write_through", nbytes, True), ("ordinary", nbytes, False),
+                            ("empty", 0, True)):
+        t = lab.measure_store_floor(y, n, grid, 512, lds, through, warmup=warmup,
+                                    min_warmup_ms=min_warmup_ms, iterations=steps,
+                                    launches_per_graph=min(steps, 100))
+        us = t["mean_ms"] * 1e3
+        out[f"{key}_us_per_launch"] = round(us, 3)
+        if n:
+            units = y.download(np.int32, n // 4).reshape(-1, 4)
+            if not (units == np.arange(units.shape[0], dtype=np.int32)[:, None]).all():
+                print(f"bench.py: the store floor kernel ({key}) left wrong bytes", file=sys.stderr)
+                return 1
+    us = out["write_through_us_per_launch"]
+    out["tops_if_conv_took_this_long"] = round(shape.ops() / (us * 1e-6) / 1e12, 1)
+    out["pct_int8_mfma_peak_at_floor"] = round(100 * shape.ops() / (us * 1e-6) / 1e12
+                                               / PEAK_INT8_TOPS, 2)
+    y.close()
+    print(json.dumps(out), flush=True)
     return 0
 
 
@@ -154,12 +213,13 @@ def traffic_record(workload: str, kernel: str):
 
 
 def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[1])
     ap.add_argument("--gpus", type=int, default=1)
-    # the clocks settle after ~20 ms of back-to-back launches: 10000 warmup
-    # launches (~65 ms) before the 5000 timed ones (~33 ms)
-    ap.add_argument("--steps", type=int, default=5000)
-    ap.add_argument("--warmup", type=int, default=10000)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--min-warmup-ms", type=float, default=100.0,
+                    help="wall time the warmup lasts at least, whatever --warmup says "
+                         "(the clocks settle after some tens of ms of back-to-back launches)")
     ap.add_argument("--kernel", default="dispatch",
                     help="dispatch (default) or one of generic|strip|halo|splitk")
     ap.add_argument("--workload", default=WORKLOAD)
@@ -169,25 +229,26 @@ def main() -> int:
                          "(int32 negate: reads and writes MIB MiB) --steps times, to scale "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
     ap.add_argument("--write-floor", action="store_true",
-                    help="instead of the benchmark, time a plain fill kernel writing exactly "
-                         "the workload's int32 output bytes (the store traffic alone)")
+                    help="instead of the benchmark, time the lab's store-only kernel writing "
+                         "exactly the workload's int32 output bytes in the dispatched row "
+                         "kernel's launch shape (and an empty kernel of that shape)")
     ap.add_argument("--requant", action="store_true",
                     help="instead of the benchmark, time the same layer with requantized int8 "
                          "output (a separate line; the headline contract is int32 output)")
     args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this lab measures one GPU "
+              "(each box has one MI355X; the layer is not sharded across GPUs)", file=sys.stderr)
+        return 2
+    if args.steps <= 0 or args.warmup < 0 or args.min_warmup_ms < 0:
+        print("bench.py: --steps must be > 0, --warmup and --min-warmup-ms >= 0", file=sys.stderr)
+        return 2
     if args.requant:
         return requant_bench(args.workload, args.steps, args.warmup)
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration, args.steps)
     if args.write_floor:
-        return write_floor(args.workload, args.steps, args.warmup)
-    if args.gpus != 1:
-        print(f"bench.py: --gpus {args.gpus} is not supported: this lab measures one GPU "
-              "(each box has one MI355X; the layer is not sharded across GPUs)", file=sys.stderr)
-        return 2
-    if args.steps <= 0 or args.warmup < 0:
-        print("bench.py: --steps must be > 0 and --warmup >= 0", file=sys.stderr)
-        return 2
+        return write_floor(args.workload, args.steps, args.warmup, args.min_warmup_ms)
 
     import numpy as np
     import int8_kernel_lab_amd as lab
@@ -208,20 +269,29 @@ def main() -> int:
     lab.synchronize()
     got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
     expected = oracle.conv(shape, x, w, b)
-    if not np.array_equal(got, expected):
+    if not np.array_equal(got, expected) or lab.wait_expired():
         print(f"bench.py: {kernel} output differs from the oracle on {args.workload}",
               file=sys.stderr)
         return 1
 
-    median_ms, stream_ms = lab.measure(kernel, shape, xb, wb, bb, yb, ws, ws_n,
-                                       warmup=args.warmup, iterations=args.steps)
-    per_graph = 100 if args.steps % 100 == 0 else 1
-    yb.fill(0xA5)
-    mean_ms = lab.measure_graph(kernel, shape, xb, wb, bb, yb, ws, ws_n, warmup=args.warmup,
-                                iterations=args.steps, launches_per_graph=per_graph)
+    # the timed steps: graph replays; the output is poisoned right before
+    # them, so the check afterwards covers exactly the timed launches
+    per_graph = min(args.steps, 100)
+    t = lab.measure_graph(kernel, shape, xb, wb, bb, yb, ws, ws_n, warmup=args.warmup,
+                          min_warmup_ms=args.min_warmup_ms, iterations=args.steps,
+                          launches_per_graph=per_graph, poison_byte=0xA5)
+    mean_ms = t["mean_ms"]
     got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
     if not np.array_equal(got, expected):
-        print(f"bench.py: {kernel} output after the graph replays differs from the oracle",
+        print(f"bench.py: {kernel} output after the timed replays differs from the oracle",
+              file=sys.stderr)
+        return 1
+    # beside it, right after (the clocks are warm): the same launches on a
+    # stream one by one, and the reference's per-launch median
+    median_ms, stream_ms = lab.measure(kernel, shape, xb, wb, bb, yb, ws, ws_n,
+                                       warmup=args.warmup, iterations=args.steps)
+    if lab.wait_expired():
+        print(f"bench.py: a bounded wait of {kernel} gave up during the timed launches",
               file=sys.stderr)
         return 1
     ops = shape.ops()
@@ -229,8 +299,10 @@ def main() -> int:
     tops = ops / (mean_ms * 1e-3) / 1e12
     gbps = nbytes / (mean_ms * 1e-3) / 1e9
     info = lab.device_info()
-    threads = min(16, os.cpu_count() or 1)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(shape, x, w, b, threads)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(shape, x, w, b)
+    graphs = f"{t['full_replays']} replay(s) of a HIP graph of {t['launches_per_graph']} launches"
+    if t["remainder_launches"]:
+        graphs += f" + a graph of {t['remainder_launches']}"
 
     line = {
         "metric": "effective INT8 TOPS per conv layer + % of MI355X dense INT8 MFMA peak",
@@ -249,16 +321,18 @@ def main() -> int:
             "workload": f"{args.workload}: N={shape.n} H=W={shape.h} C={shape.c} K={shape.k} "
                         f"{shape.r}x{shape.s} stride {shape.stride_h} pad {shape.pad_h}",
             "kernel": kernel,
+            "plan": lab.describe(kernel, shape),
             "gemm_mnk": [g.gemm_m, g.gemm_n, g.gemm_k],
             "ops_per_step": ops,
             "algorithmic_bytes_per_step": nbytes,
             "pct_int8_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
-            "per_launch_median_ms": round(median_ms, 6),
-            "timing": f"HIP graph of {per_graph} launches replayed; "
-                      f"{args.steps} launches enqueued one by one on a stream: "
-                      f"{stream_ms * 1e3:.3f} us per launch "
-                      f"({ops / (stream_ms * 1e-3) / 1e12:.1f} TOPS)",
+            "timing": f"{args.steps} back-to-back launches timed as {graphs}, after "
+                      f"{t['warmup_launches']} warmup launches over {t['warmup_ms']:.0f} ms; "
+                      f"output poisoned before and checked after the timed launches",
+            "warmup_launches_run": t["warmup_launches"],
+            "warmup_ms": round(t["warmup_ms"], 1),
             "stream_ms_per_step": round(stream_ms, 6),
+            "per_launch_median_ms": round(median_ms, 6),
             "device": info["arch"],
             "compute_units": info["compute_units"],
             "parallelism": "single GPU",

@@ -214,23 +214,70 @@ int i8conv_synchronize(void);
 int i8conv_stream_create(void **stream);
 int i8conv_stream_destroy(void *stream);
 
+/* No counterpart in the reference.  The row kernel with copy waves (the
+ * halo kernel's form for 128-channel 3x3 layers) makes its compute waves
+ * wait for copy waves through LDS counters; each wait is bounded (about
+ * 2^20 polls, tens of ms) so that every wave ends, and a wave whose wait
+ * runs out sets a device word.  This call synchronizes the current device,
+ * reads that word into *expired (1: some launch since the last call gave up
+ * waiting, and its output must be treated as wrong; 0: none did) and
+ * clears it. */
+int i8conv_wait_expired(int *expired);
+
 /* Device facts for roofline reporting: compute units, peak engine clock in
  * kHz, gcnArchName (at most `name_len` bytes incl. NUL). */
 int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
                        size_t name_len);
 
+/* Result of i8conv_measure_graph. */
+typedef struct i8conv_graph_timing {
+  float mean_ms;          /* timed elapsed / iterations */
+  int launches_per_graph; /* launches in the main graph */
+  int full_replays;       /* replays of the main graph in the timed region */
+  int remainder_launches; /* launches of the remainder graph (0: none) */
+  int warmup_launches;    /* launches replayed before the timed region */
+  float warmup_ms;        /* host wall time of the warmup */
+} i8conv_graph_timing;
+
 /* No counterpart in the reference, which times launches one by one
- * (conv_lab.cu:88-110).  Back-to-back launches replayed from a HIP graph:
- * one launch on a stream of its own (default priority), then a graph of
- * `launches_per_graph` i8conv_launch calls (kernel nodes only) captured on
- * it; ceil(warmup / launches_per_graph) replays, synchronize, then
- * iterations / launches_per_graph replays between one event pair.
- * *mean_ms = elapsed / iterations.  iterations must be a positive multiple
- * of launches_per_graph.  Synchronous; the output holds the last launch's. */
+ * (conv_lab.cu:88-110).  Back-to-back launches replayed from HIP graphs, on
+ * a stream of its own (default priority):
+ *   1. one launch outside any graph, synchronized;
+ *   2. when poison_byte >= 0, the output is filled with that byte (outside
+ *      any graph, synchronous);
+ *   3. a main graph of L = min(launches_per_graph, iterations)
+ *      i8conv_launch calls is captured (kernel nodes only), and a
+ *      remainder graph of iterations % L launches when that is nonzero;
+ *   4. warmup: main-graph replays until at least `warmup` launches have run
+ *      and at least min_warmup_ms of host wall time has passed;
+ *   5. the output is poisoned again (step 2), so that it then holds only
+ *      what the timed replays wrote;
+ *   6. timed region: iterations / L main-graph replays plus the remainder
+ *      graph, exactly `iterations` launches, between one event pair.
+ * Fills *timing.  Synchronous. */
 int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
                          const int8_t *filter, const int32_t *bias, int32_t *output,
                          void *workspace, size_t workspace_bytes, int warmup,
-                         int iterations, int launches_per_graph, float *mean_ms);
+                         double min_warmup_ms, int iterations,
+                         int launches_per_graph, int poison_byte,
+                         i8conv_graph_timing *timing);
+
+/* No counterpart in the reference: the store floor of a launch shape.  A
+ * kernel that only writes `bytes` of `output` (16-byte aligned, a multiple
+ * of 16 below 2^31) with 16-byte buffer stores, write-through when
+ * write_through != 0 (the row kernels' output policy) else ordinary, in
+ * `workgroups` x threads_per_workgroup (whole waves, at most 1024) with
+ * lds_bytes of dynamic LDS allocated and unused; timed as
+ * i8conv_measure_graph times a convolution (poison byte 0x5A).  16-byte
+ * unit u of the output ends up holding the int32 value u four times.
+ * bytes == 0 times an empty kernel of the launch shape (the dispatch
+ * floor).  Synchronous. */
+int i8conv_measure_store_floor(int32_t *output, size_t bytes, int workgroups,
+                               int threads_per_workgroup, size_t lds_bytes,
+                               int write_through, int warmup,
+                               double min_warmup_ms, int iterations,
+                               int launches_per_graph,
+                               i8conv_graph_timing *timing);
 
 /* measure() (conv_lab.cu:88-110): `warmup` launches, synchronize; when
  * batched_ms is non-NULL, `iterations` back-to-back launches between one

@@ -37,7 +37,7 @@ __all__ = [
     "WORKLOADS_DIR", "BASELINE_SEED", "device_count", "device_info", "set_device",
     "synchronize", "requantize", "requant_fused", "requant_workspace_bytes", "launch_requant",
     "conv2d_requant", "measure_requant", "nchw_to_nhwc", "nhwc_to_nchw", "nhwk_to_nkhw",
-    "pack_vect_c", "unpack_vect_c",
+    "pack_vect_c", "unpack_vect_c", "measure_graph", "measure_store_floor", "wait_expired",
 ]
 
 KERNELS = ("generic", "strip", "halo", "splitk")
@@ -304,19 +304,52 @@ def measure(name: str, shape: ConvShape, input, filter, bias, output, workspace=
 
 def measure_graph(name: str, shape: ConvShape, input, filter, bias, output, workspace=None,
                   workspace_nbytes: int = 0, warmup: int = 10000, iterations: int = 5000,
-                  launches_per_graph: int = 100) -> float:
-    """Mean ms per launch of `iterations` back-to-back launches replayed from
-    a HIP graph of `launches_per_graph` launches (i8conv_measure_graph)."""
+                  launches_per_graph: int = 100, min_warmup_ms: float = 0.0,
+                  poison_byte: int = -1) -> Dict[str, float]:
+    """`iterations` back-to-back launches replayed from HIP graphs
+    (i8conv_measure_graph): a main graph of min(launches_per_graph,
+    iterations) launches plus a remainder graph, after a warmup of at least
+    `warmup` launches and `min_warmup_ms` of wall time; with poison_byte >= 0
+    the output is poisoned before the capture and again right before the
+    timed replays, so that afterwards it holds only what they wrote.
+    Returns the i8conv_graph_timing fields as a dict (mean_ms per launch)."""
     if isinstance(workspace, DeviceBuffer) and not workspace_nbytes:
         workspace_nbytes = workspace.nbytes
-    mean = ctypes.c_float()
+    t = _lib.CGraphTiming()
     status = lib().i8conv_measure_graph(_kernel_id(name), ctypes.byref(shape.c_struct()),
                                         _ptr(input), _ptr(filter), _ptr(bias), _ptr(output),
                                         _ptr(workspace), int(workspace_nbytes), int(warmup),
-                                        int(iterations), int(launches_per_graph),
-                                        ctypes.byref(mean))
+                                        float(min_warmup_ms), int(iterations),
+                                        int(launches_per_graph), int(poison_byte),
+                                        ctypes.byref(t))
     check(status, f"measure_graph {name}")
-    return mean.value
+    return {f: getattr(t, f) for f, _ in _lib.CGraphTiming._fields_}
+
+
+def measure_store_floor(output, nbytes: int, workgroups: int = 256, threads: int = 512,
+                        lds_bytes: int = 0, write_through: bool = True, warmup: int = 0,
+                        min_warmup_ms: float = 100.0, iterations: int = 1000,
+                        launches_per_graph: int = 100) -> Dict[str, float]:
+    """Times a store-only kernel writing `nbytes` of `output` in the given
+    launch shape (i8conv_measure_store_floor): the floor under any kernel of
+    that shape that writes that output.  nbytes = 0: an empty kernel."""
+    t = _lib.CGraphTiming()
+    check(lib().i8conv_measure_store_floor(_ptr(output), int(nbytes), int(workgroups),
+                                           int(threads), int(lds_bytes), int(write_through),
+                                           int(warmup), float(min_warmup_ms), int(iterations),
+                                           int(launches_per_graph), ctypes.byref(t)),
+          "measure_store_floor")
+    return {f: getattr(t, f) for f, _ in _lib.CGraphTiming._fields_}
+
+
+def wait_expired() -> bool:
+    """True when a row-kernel wave's bounded wait gave up since the last call
+    (i8conv_wait_expired: synchronizes the device, reads and clears the
+    word); the outputs of the launches since then are then not to be
+    trusted."""
+    flag = ctypes.c_int()
+    check(lib().i8conv_wait_expired(ctypes.byref(flag)), "wait_expired")
+    return bool(flag.value)
 
 
 def device_info() -> Dict[str, object]:

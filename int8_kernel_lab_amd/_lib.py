@@ -8,7 +8,8 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint64, c_void_p
+from ctypes import (POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t,
+                    c_uint32, c_uint64, c_void_p)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libi8conv.so")
@@ -38,6 +39,14 @@ class CGeometry(ctypes.Structure):
                 ("gemm_n", c_int32), ("gemm_k", c_int32),
                 ("input_elements", c_int64), ("filter_elements", c_int64),
                 ("output_elements", c_int64)]
+
+
+class CGraphTiming(ctypes.Structure):
+    """struct i8conv_graph_timing (result of i8conv_measure_graph)."""
+
+    _fields_ = [("mean_ms", c_float), ("launches_per_graph", c_int), ("full_replays", c_int),
+                ("remainder_launches", c_int), ("warmup_launches", c_int),
+                ("warmup_ms", c_float)]
 
 
 # name -> (restype, argtypes); every symbol include/i8conv.h declares.
@@ -87,10 +96,14 @@ SIGNATURES = {
     "i8conv_synchronize": (c_int, []),
     "i8conv_stream_create": (c_int, [POINTER(c_void_p)]),
     "i8conv_stream_destroy": (c_int, [c_void_p]),
+    "i8conv_wait_expired": (c_int, [POINTER(c_int)]),
     "i8conv_device_info": (c_int, [POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]),
     "i8conv_measure_graph": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,
-                                     c_void_p, c_void_p, c_size_t, c_int, c_int, c_int,
-                                     POINTER(c_float)]),
+                                     c_void_p, c_void_p, c_size_t, c_int, c_double, c_int,
+                                     c_int, c_int, POINTER(CGraphTiming)]),
+    "i8conv_measure_store_floor": (c_int, [c_void_p, c_size_t, c_int, c_int, c_size_t, c_int,
+                                           c_int, c_double, c_int, c_int,
+                                           POINTER(CGraphTiming)]),
     "i8conv_measure": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,
                                c_void_p, c_void_p, c_size_t, c_void_p, c_int, c_int,
                                POINTER(c_float), POINTER(c_float)]),

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <initializer_list>
 #include <string>
 #include <vector>
@@ -77,6 +78,106 @@ int measure_loop(Launch launch, void *stream, int warmup, int iterations, float 
   // teardown: a failure here cannot change the measured result
   (void)hipEventDestroy(start);
   (void)hipEventDestroy(stop);
+  return rc;
+}
+
+// Back-to-back launches replayed from HIP graphs on a stream of its own
+// (default priority), the steps documented at i8conv_measure_graph:
+// a launch outside any graph, poison, capture of a main graph (and of a
+// remainder graph), warmup replays until `warmup` launches and
+// min_warmup_ms of wall time, poison, then exactly `iterations` launches
+// between one event pair.  launch(stream) enqueues one launch.
+template <class Launch>
+int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup,
+                       double min_warmup_ms, int iterations, int launches_per_graph,
+                       int poison_byte, i8conv_graph_timing *timing) {
+  const int per_graph = std::min(launches_per_graph, iterations);
+  const int full_replays = iterations / per_graph;
+  const int remainder = iterations - full_replays * per_graph;
+  *timing = i8conv_graph_timing{};
+
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);  // default priority
+  if (e != hipSuccess) return hip_fail("hipStreamCreateWithFlags", e);
+  hipGraph_t graphs[2] = {nullptr, nullptr};
+  hipGraphExec_t execs[2] = {nullptr, nullptr};
+  hipEvent_t start = nullptr, stop = nullptr;
+  // poisons the output outside any graph (synchronous), so that a check
+  // after the replays sees only what the replays wrote
+  auto poison = [&]() {
+    if (poison_byte < 0 || out_bytes == 0) return int(I8CONV_OK);
+    hipError_t pe = hipMemsetAsync(output, poison_byte, out_bytes, s);
+    if (pe == hipSuccess) pe = hipStreamSynchronize(s);
+    return pe == hipSuccess ? int(I8CONV_OK) : hip_fail("poison", pe);
+  };
+  // captures `count` launches (kernel nodes only) into graphs[slot]
+  auto capture = [&](int slot, int count) {
+    hipError_t ce = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
+    if (ce != hipSuccess) return hip_fail("hipStreamBeginCapture", ce);
+    int crc = I8CONV_OK;
+    for (int i = 0; i < count && crc == I8CONV_OK; ++i) crc = launch(s);
+    // end the capture whatever happened inside it
+    ce = hipStreamEndCapture(s, &graphs[slot]);
+    if (crc == I8CONV_OK && ce != hipSuccess) crc = hip_fail("hipStreamEndCapture", ce);
+    if (crc == I8CONV_OK &&
+        (ce = hipGraphInstantiate(&execs[slot], graphs[slot], nullptr, nullptr, 0)) != hipSuccess)
+      crc = hip_fail("hipGraphInstantiate", ce);
+    return crc;
+  };
+  // one launch outside the graphs (checks the arguments, sets any function
+  // attribute the kernel needs), then the poison, then the captures
+  int rc = launch(s);
+  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("launch", e);
+  if (rc == I8CONV_OK) rc = poison();
+  if (rc == I8CONV_OK) rc = capture(0, per_graph);
+  if (rc == I8CONV_OK && remainder > 0) rc = capture(1, remainder);
+  // warmup: replays of the main graph until at least `warmup` launches have
+  // run and at least min_warmup_ms of wall time has passed (back-to-back
+  // launches need some tens of ms to bring the clocks to their steady
+  // state); batches of replays between host checks, doubling up to 64
+  int warm_launches = 0;
+  double warm_ms = 0.0;
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int batch = 1; rc == I8CONV_OK && (warm_launches < warmup || warm_ms < min_warmup_ms);) {
+    for (int i = 0; i < batch && rc == I8CONV_OK; ++i)
+      if ((e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
+    if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("warmup", e);
+    warm_launches += batch * per_graph;
+    warm_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
+                  .count();
+    batch = std::min(2 * batch, 64);
+  }
+  if (rc == I8CONV_OK) rc = poison();
+  if (rc == I8CONV_OK && (e = hipEventCreate(&start)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&stop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  // the timed region: exactly `iterations` launches
+  if (rc == I8CONV_OK && (e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  for (int i = 0; i < full_replays && rc == I8CONV_OK; ++i)
+    if ((e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
+  if (rc == I8CONV_OK && remainder > 0 && (e = hipGraphLaunch(execs[1], s)) != hipSuccess)
+    rc = hip_fail("hipGraphLaunch", e);
+  if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
+  float ms = 0.f;
+  if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess)
+    rc = hip_fail("hipEventElapsedTime", e);
+  if (rc == I8CONV_OK) {
+    timing->mean_ms = ms / float(iterations);
+    timing->launches_per_graph = per_graph;
+    timing->full_replays = full_replays;
+    timing->remainder_launches = remainder;
+    timing->warmup_launches = warm_launches;
+    timing->warmup_ms = float(warm_ms);
+  }
+  // teardown: drain the stream first; a failure here cannot change the result
+  (void)hipStreamSynchronize(s);
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  for (int i = 0; i < 2; ++i) {
+    if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
+    if (graphs[i]) (void)hipGraphDestroy(graphs[i]);
+  }
+  (void)hipStreamDestroy(s);
   return rc;
 }
 }  // namespace
@@ -511,6 +612,14 @@ int i8conv_stream_destroy(void *stream) {
   return e == hipSuccess ? I8CONV_OK : hip_fail("hipStreamDestroy", e);
 }
 
+int i8conv_wait_expired(int *expired) {
+  if (!expired) {
+    set_error("wait_expired needs an output");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  return rowpass_wait_expired(expired);
+}
+
 int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
                        size_t name_len) {
   int dev = 0;
@@ -545,62 +654,48 @@ int i8conv_measure(int id, const i8conv_shape *shape, const int8_t *input,
 
 int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
                          const int8_t *filter, const int32_t *bias, int32_t *output,
-                         void *workspace, size_t workspace_bytes, int warmup, int iterations,
-                         int launches_per_graph, float *mean_ms) {
-  if (warmup < 0 || iterations <= 0 || launches_per_graph <= 0 || !mean_ms ||
-      iterations % launches_per_graph != 0) {
-    set_error("measure_graph needs warmup >= 0, iterations a positive multiple of "
-              "launches_per_graph, and an output");
+                         void *workspace, size_t workspace_bytes, int warmup,
+                         double min_warmup_ms, int iterations, int launches_per_graph,
+                         int poison_byte, i8conv_graph_timing *timing) {
+  if (warmup < 0 || !(min_warmup_ms >= 0.0) || iterations <= 0 || launches_per_graph <= 0 ||
+      poison_byte > 255 || !timing) {
+    set_error("measure_graph needs warmup >= 0, min_warmup_ms >= 0, iterations > 0, "
+              "launches_per_graph > 0, poison_byte < 256 and a timing record");
     return I8CONV_BAD_ARGUMENT;
   }
-  hipStream_t s = nullptr;
-  hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
-  if (e != hipSuccess) return hip_fail("hipStreamCreateWithFlags", e);
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  hipEvent_t start = nullptr, stop = nullptr;
-  auto launch = [&]() {
-    return i8conv_launch(id, shape, input, filter, bias, output, workspace, workspace_bytes, s);
-  };
-  // one launch outside the graph (checks the arguments, sets any function
-  // attribute the kernel needs), then the capture of launches_per_graph
-  // launches: kernel nodes only
-  int rc = launch();
-  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("launch", e);
-  if (rc == I8CONV_OK &&
-      (e = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed)) != hipSuccess)
-    rc = hip_fail("hipStreamBeginCapture", e);
-  if (rc == I8CONV_OK) {
-    for (int i = 0; i < launches_per_graph && rc == I8CONV_OK; ++i) rc = launch();
-    // end the capture whatever happened inside it
-    const hipError_t ec = hipStreamEndCapture(s, &graph);
-    if (rc == I8CONV_OK && ec != hipSuccess) rc = hip_fail("hipStreamEndCapture", ec);
+  i8conv_geometry g{};
+  if (const int rc = i8conv_derive(shape, &g); rc != I8CONV_OK) return rc;
+  return measure_graph_loop(
+      [&](hipStream_t s) {
+        return i8conv_launch(id, shape, input, filter, bias, output, workspace, workspace_bytes,
+                             s);
+      },
+      output, size_t(g.output_elements) * sizeof(int32_t), warmup, min_warmup_ms, iterations,
+      launches_per_graph, poison_byte, timing);
+}
+
+int i8conv_measure_store_floor(int32_t *output, size_t bytes, int workgroups,
+                               int threads_per_workgroup, size_t lds_bytes, int write_through,
+                               int warmup, double min_warmup_ms, int iterations,
+                               int launches_per_graph, i8conv_graph_timing *timing) {
+  if (!output || bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(output) & 15) != 0 ||
+      bytes >= (size_t(1) << 31) || workgroups <= 0 || threads_per_workgroup <= 0 ||
+      threads_per_workgroup > 1024 || threads_per_workgroup % 64 != 0 ||
+      lds_bytes > size_t(kLdsBudget) || warmup < 0 || !(min_warmup_ms >= 0.0) ||
+      iterations <= 0 || launches_per_graph <= 0 || !timing) {
+    set_error("measure_store_floor needs a 16-byte aligned output, bytes a multiple of 16 below "
+              "2^31, workgroups > 0, 64..1024 threads in whole waves, lds_bytes within the LDS "
+              "budget, warmup >= 0, min_warmup_ms >= 0, iterations and launches_per_graph > 0 "
+              "and a timing record");
+    return I8CONV_BAD_ARGUMENT;
   }
-  if (rc == I8CONV_OK && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
-    rc = hip_fail("hipGraphInstantiate", e);
-  const int warm_replays = (warmup + launches_per_graph - 1) / launches_per_graph;
-  for (int i = 0; i < warm_replays && rc == I8CONV_OK; ++i)
-    if ((e = hipGraphLaunch(exec, s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
-  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("warmup", e);
-  if (rc == I8CONV_OK && (e = hipEventCreate(&start)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
-  if (rc == I8CONV_OK && (e = hipEventCreate(&stop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
-  if (rc == I8CONV_OK && (e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-  for (int i = 0; i < iterations / launches_per_graph && rc == I8CONV_OK; ++i)
-    if ((e = hipGraphLaunch(exec, s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
-  if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-  if (rc == I8CONV_OK && (e = hipEventSynchronize(stop)) != hipSuccess) rc = hip_fail("hipEventSynchronize", e);
-  float ms = 0.f;
-  if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess)
-    rc = hip_fail("hipEventElapsedTime", e);
-  if (rc == I8CONV_OK) *mean_ms = ms / float(iterations);
-  // teardown: drain the stream first; a failure here cannot change the result
-  (void)hipStreamSynchronize(s);
-  if (start) (void)hipEventDestroy(start);
-  if (stop) (void)hipEventDestroy(stop);
-  if (exec) (void)hipGraphExecDestroy(exec);
-  if (graph) (void)hipGraphDestroy(graph);
-  (void)hipStreamDestroy(s);
-  return rc;
+  // a first launch sets the LDS attribute the shape may need
+  return measure_graph_loop(
+      [&](hipStream_t s) {
+        return launch_store_floor(output, bytes, workgroups, threads_per_workgroup, lds_bytes,
+                                  write_through != 0, s);
+      },
+      output, bytes, warmup, min_warmup_ms, iterations, launches_per_graph, 0x5A, timing);
 }
 
 int i8conv_measure_requant(const i8conv_shape *shape, const int8_t *input, const int8_t *filter,

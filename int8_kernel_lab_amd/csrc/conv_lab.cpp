@@ -244,12 +244,25 @@ int main(int argc, char **argv) {
     check(i8conv_synchronize(), name);
     check(i8conv_copy_to_host(got.data(), d_y, got.size() * 4), "copy output");
     r.correct = validate(expected, got, name);
+    // a bounded wait that gave up means data the kernel read had not landed
+    int expired = 0;
+    check(i8conv_wait_expired(&expired), name);
+    if (expired) {
+      std::cerr << name << ": a bounded wait inside the kernel gave up\n";
+      r.correct = false;
+    }
     if (r.correct) {
       check(i8conv_measure(id, &shape, static_cast<int8_t *>(d_x), static_cast<int8_t *>(d_w),
                            static_cast<int32_t *>(d_b), static_cast<int32_t *>(d_y), d_ws,
                            ws_bytes, nullptr, opt.warmup, opt.iterations, &r.ms,
                            &r.batched_ms),
             name);
+      check(i8conv_wait_expired(&expired), name);
+      if (expired) {
+        std::cerr << name << ": a bounded wait gave up during the timed launches\n";
+        r.correct = false;
+        r.ms = -1.0f;
+      }
     }
   }
 

@@ -175,14 +175,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // compiler does not model it: it would otherwise wait for every copy in
 // flight before any later LDS read.  The caller owns the vmcnt accounting
 // (these copies complete in issue order with the wave's other vector
-// memory loads).  M0 is set here and used by nothing else in these kernels.
+// memory loads).  The LDS address goes in as an M0 operand: the compiler
+// writes M0 itself right before the asm (and so knows it is in use), and
+// the asm's s_nop gives that write the wait state the copy needs.
 __device__ __forceinline__ void lds_copy16(v4u desc, uint32_t lds_base, uint32_t voffset) {
   asm volatile(
-      "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
       :
-      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voffset), "s"(desc)
+      : "v"(voffset), "s"(desc), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
       : "memory");
 }
 
@@ -190,11 +191,10 @@ __device__ __forceinline__ void lds_copy16(v4u desc, uint32_t lds_base, uint32_t
 // `voffset` lands at lds_base + 4*i (zero when out of range).
 __device__ __forceinline__ void lds_copy4(v4u desc, uint32_t lds_base, uint32_t voffset) {
   asm volatile(
-      "s_mov_b32 m0, %0\n\t"
       "s_nop 0\n\t"
-      "buffer_load_dword %1, %2, 0 offen lds"
+      "buffer_load_dword %0, %1, 0 offen lds"
       :
-      : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voffset), "s"(desc)
+      : "v"(voffset), "s"(desc), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
       : "memory");
 }
 

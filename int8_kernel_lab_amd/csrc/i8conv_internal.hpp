@@ -116,6 +116,14 @@ int rowpass_nfr(int out_w);
 // ... and the most output rows per block it has an instance for
 int rowpass_max_rows(int nfr);
 size_t rowpass_lds_bytes(int wp, int rows);
+// kernel_rowpass.hip: reads and clears the device word its waves set when a
+// bounded wait gives up (synchronizes the device); *expired = 1 if it was set.
+int rowpass_wait_expired(int *expired);
+// kernel_probe.hip: a store-only kernel (16-byte buffer stores, write-through
+// or ordinary) over `bytes` of y (a multiple of 16, below 2^31) in the
+// launch shape workgroups x threads with `lds` bytes of dynamic LDS.
+int launch_store_floor(int32_t *y, size_t bytes, int workgroups, int threads, size_t lds,
+                       bool write_through, void *stream);
 // Whether kernel_row.hip has an instance for 16*fn channels per wave, cg
 // 64-channel groups and nfr 16-column fragments per output row.
 bool row_instance_exists(int fn, int cg, int nfr);

@@ -41,6 +41,11 @@
 #include "halo_common.hpp"
 
 namespace i8conv {
+
+// Set by a wave of rowpass_kernel whose bounded chunk wait gave up (below);
+// read and cleared by rowpass_wait_expired on the host.
+__device__ __attribute__((aligned(4))) unsigned int g_wait_expired;
+
 namespace {
 
 constexpr int kGroups = 2;      // 64-channel groups: c == 128
@@ -77,8 +82,14 @@ struct PassArgs {
 // Cross-wave signals in LDS: a copy wave adds 1 to a chunk's counter once
 // its copies of that chunk have landed (its own vmcnt says so: LDS-DMA data
 // is in LDS when the count drops), and the MFMA waves poll the counter.
-// The wait is bounded: after kSpinLimit polls (far beyond any real copy
-// time) it gives up, so every wave always reaches the end of the kernel.
+// The wait is bounded: after kSpinLimit polls (each a read and a sleep of
+// about 64 cycles, some tens of ms in all, far beyond any real copy time) it
+// gives up, so that every wave always reaches the end of the kernel.  A
+// wave that gives up goes on with LDS contents that may not have landed,
+// so it records the give-up in g_wait_expired (a vector store to global
+// memory); the host reads and clears that word with i8conv_wait_expired()
+// after synchronizing, and must treat the output of the launches since the
+// last check as wrong when it is set.
 constexpr int kSpinLimit = 1 << 20;
 constexpr int kCopyWaves = 4;
 
@@ -101,6 +112,9 @@ __device__ __forceinline__ void flag_wait(uint32_t addr, int target) {
     if (__builtin_amdgcn_readfirstlane(v) >= target) return;
     __builtin_amdgcn_s_sleep(1);
   }
+  // the chunk never arrived: every lane stores the same word (one vector
+  // store), the host finds it set after the launch
+  *reinterpret_cast<volatile unsigned int *>(&g_wait_expired) = 1u;
 }
 
 // State of one wave's row walk over output rows [OLO, OHI) of the block
@@ -206,6 +220,11 @@ struct PassState {
       const int seen = peeked;
       if (IR + 2 < OHI + 2) peeked = flag_peek(counter<G>(p, IR + 2));
       if (seen < kCopyWaves) flag_wait(counter<G>(p, IR + 1), kCopyWaves);
+      // keeps the compiler from moving the plain LDS reads of load_row (and
+      // take_taps) above the counter check on the path that skips
+      // flag_wait (whose asm already orders them); the hardware issues a
+      // wave's LDS operations in order, so no wait instruction is needed
+      asm volatile("" ::: "memory");
       constexpr int fy_next = IR + 1 - OLO;
       if (fy_next <= 2) take_taps<G, (fy_next <= 2 ? fy_next : 0)>(lane);
       load_row<G>(p, IR + 1);
@@ -676,6 +695,26 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream, const Re
 #undef I8_PASS_CASE
   set_error("no row-kernel (copy waves) instance for this plan");
   return I8CONV_BAD_ARGUMENT;
+}
+
+int rowpass_wait_expired(int *expired) {
+  void *word = nullptr;
+  hipError_t e = hipGetSymbolAddress(&word, HIP_SYMBOL(g_wait_expired));
+  if (e != hipSuccess) {
+    set_error(std::string("hipGetSymbolAddress(g_wait_expired): ") + hipGetErrorString(e));
+    return I8CONV_HIP_ERROR;
+  }
+  e = hipDeviceSynchronize();
+  unsigned int value = 0;
+  if (e == hipSuccess) e = hipMemcpy(&value, word, sizeof(value), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && value != 0) e = hipMemset(word, 0, sizeof(value));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    set_error(std::string("reading g_wait_expired: ") + hipGetErrorString(e));
+    return I8CONV_HIP_ERROR;
+  }
+  *expired = value != 0 ? 1 : 0;
+  return I8CONV_OK;
 }
 
 }  // namespace i8conv

@@ -34,6 +34,20 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#ifndef ORACLE_CFLAGS
+#define ORACLE_CFLAGS "unknown"
+#endif
+
+/* Compiler and flags this library was built with (reported beside CPU
+ * timings of the oracle). */
+const char *oracle_build_info(void) {
+#if defined(__VERSION__)
+  return "cc " __VERSION__ ", " ORACLE_CFLAGS;
+#else
+  return "cc (unknown version), " ORACLE_CFLAGS;
+#endif
+}
+
 typedef struct oracle_shape {
   int32_t n, h, w, c, k, r, s;
   int32_t pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w;

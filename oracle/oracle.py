@@ -8,7 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_int, c_int32, c_int64, c_void_p
+from ctypes import c_char_p, POINTER, c_int, c_int32, c_int64, c_void_p
 
 import numpy as np
 
@@ -56,8 +56,15 @@ def lib():
         h.oracle_requantize.restype = None
         h.oracle_requantize.argtypes = [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,
                                         c_void_p]
+        h.oracle_build_info.restype = c_char_p
+        h.oracle_build_info.argtypes = []
         _lib = h
     return _lib
+
+
+def build_info() -> str:
+    """Compiler version and flags liboracle.so was built with."""
+    return lib().oracle_build_info().decode()
 
 
 def _shape(shape) -> OShape:

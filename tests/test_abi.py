@@ -232,6 +232,30 @@ def test_launch_errors_without_touching_the_gpu(baseline_cases):
                                                None, 0, None) == _lib.BAD_SHAPE
 
 
+def test_measure_graph_argument_errors_without_touching_the_gpu(baseline_cases):
+    # i8conv_measure_graph checks its counts, poison byte, timing record and
+    # shape before any HIP call
+    cfg2 = baseline_cases["cfg2_resnet_3x3_s1"].c_struct()
+    t = _lib.CGraphTiming()
+
+    def call(shape=cfg2, warmup=0, min_ms=0.0, iterations=20, per_graph=20, poison=-1,
+             timing=True):
+        return _lib.lib().i8conv_measure_graph(
+            2, ctypes.byref(shape), FAKE, FAKE, FAKE, FAKE, None, 0, warmup, min_ms,
+            iterations, per_graph, poison, ctypes.byref(t) if timing else None)
+
+    assert call(warmup=-1) == _lib.BAD_ARGUMENT
+    assert call(min_ms=-1.0) == _lib.BAD_ARGUMENT
+    assert call(min_ms=float("nan")) == _lib.BAD_ARGUMENT
+    assert call(iterations=0) == _lib.BAD_ARGUMENT
+    assert call(per_graph=0) == _lib.BAD_ARGUMENT
+    assert call(poison=256) == _lib.BAD_ARGUMENT
+    assert call(timing=False) == _lib.BAD_ARGUMENT
+    assert "poison_byte" in _lib.lib().i8conv_last_error().decode()
+    bad = lab.ConvShape(1, 8, 8, 24, 8, 3, 3, 1, 1).c_struct()
+    assert call(shape=bad) == _lib.BAD_SHAPE
+
+
 def test_python_layer_raises_on_bad_calls(baseline_cases):
     with pytest.raises(ValueError, match="unknown kernel"):
         lab.eligible("cudnn", baseline_cases["cfg1_smoke"])

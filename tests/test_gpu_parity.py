@@ -234,9 +234,11 @@ def test_launch_errors_are_statuses_not_faults(baseline_cases):
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", ["cfg2_resnet_3x3_s1", "cfg5a_deep_k"])
 def test_graph_replays_bit_exact(case, baseline_cases):
-    # the bench's timing path: launches captured in a HIP graph (split-K: two
-    # kernels per launch, the workspace rewritten every launch), replayed
-    # twice per call, two calls with the output poisoned and checked between
+    # the bench's timing path: launches captured in HIP graphs (split-K: two
+    # kernels per launch, the workspace rewritten every launch); the output
+    # is poisoned outside the graphs right before the timed replays, so the
+    # check sees only what the replays wrote.  Two calls: a main graph that
+    # divides the launches, then one with a remainder graph (7 = 2 x 3 + 1).
     shape = baseline_cases[case]
     kernel = lab.dispatch(shape)
     x, w, b, expected = _case(case, shape)
@@ -246,12 +248,15 @@ def test_graph_replays_bit_exact(case, baseline_cases):
     ws_n = lab.workspace_bytes(kernel, shape)
     ws = lab.DeviceBuffer(ws_n) if ws_n else None
     try:
-        for call in range(2):
+        for call, (iterations, per_graph) in enumerate([(6, 3), (7, 3)]):
             say(f"[gpu] graph replays {kernel} on {case}, call {call}")
-            yb.fill(0x5A + call)
-            ms = lab.measure_graph(kernel, shape, *bufs, yb, ws, ws_n, warmup=2, iterations=6,
-                                   launches_per_graph=3)
-            assert ms > 0
+            t = lab.measure_graph(kernel, shape, *bufs, yb, ws, ws_n, warmup=2,
+                                  iterations=iterations, launches_per_graph=per_graph,
+                                  min_warmup_ms=1.0, poison_byte=0x5A + call)
+            assert t["mean_ms"] > 0
+            assert t["launches_per_graph"] == per_graph
+            assert t["full_replays"] * per_graph + t["remainder_launches"] == iterations
+            assert t["warmup_launches"] >= 2 and t["warmup_ms"] >= 1.0
             got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
             assert_bit_exact(got, expected, f"graph {kernel}/{case} call {call}")
     finally:
