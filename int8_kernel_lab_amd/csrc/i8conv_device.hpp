@@ -176,11 +176,17 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // flight before any later LDS read.  The caller owns the vmcnt accounting
 // (these copies complete in issue order with the wave's other vector
 // memory loads).  The LDS address goes in as an M0 operand: the compiler
-// writes M0 itself right before the asm (and so knows it is in use), and
-// the asm's s_nop gives that write the wait state the copy needs.
+// writes M0 itself before the asm (and so knows it is in use).
+// The asm starts with s_nop 4, five wait states: a vector memory
+// instruction that reads an SGPR written by a VALU instruction (a
+// v_readlane restoring a spilled SGPR of the descriptor, a readfirstlane)
+// needs five wait states after that write, and M0 one after an SALU write.
+// The compiler's hazard check cannot see the copy inside the asm, so it
+// does not pad before it; in SGPR-heavy kernels it has placed such a
+// v_readlane two instructions before the copy.
 __device__ __forceinline__ void lds_copy16(v4u desc, uint32_t lds_base, uint32_t voffset) {
   asm volatile(
-      "s_nop 0\n\t"
+      "s_nop 4\n\t"
       "buffer_load_dwordx4 %0, %1, 0 offen lds"
       :
       : "v"(voffset), "s"(desc), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
@@ -191,7 +197,7 @@ __device__ __forceinline__ void lds_copy16(v4u desc, uint32_t lds_base, uint32_t
 // `voffset` lands at lds_base + 4*i (zero when out of range).
 __device__ __forceinline__ void lds_copy4(v4u desc, uint32_t lds_base, uint32_t voffset) {
   asm volatile(
-      "s_nop 0\n\t"
+      "s_nop 4\n\t"
       "buffer_load_dword %0, %1, 0 offen lds"
       :
       : "v"(voffset), "s"(desc), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
