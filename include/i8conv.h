@@ -140,6 +140,24 @@ int i8conv_launch_dispatched(const i8conv_shape *shape, const int8_t *input,
                              int32_t *output, void *workspace,
                              size_t workspace_bytes, void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): i8conv_launch with the workspace taken
+ * from the library's own static device scratch instead of an argument.
+ * The scratch is a file-scope device array of 16 MiB (16777216 bytes), one
+ * copy per GPU, held until the process ends; its device address is looked
+ * up on a device's first call.  A kernel/shape whose workspace exceeds 16
+ * MiB is rejected with I8CONV_WORKSPACE_TOO_SMALL (use i8conv_launch with a
+ * caller workspace).  Calls no hipMalloc/hipFree or allocating routine.
+ * Every call on a GPU shares that GPU's scratch, which keeps the last
+ * call's contents (split-K rewrites every partial sum it reads, so nothing
+ * has to start at zero): calls that overlap in time on one GPU (on
+ * different streams or host threads) race on it; calls on one stream are
+ * ordered and safe. */
+int i8conv_launch_noalloc(int id, const i8conv_shape *shape, const int8_t *input,
+                          const int8_t *filter, const int32_t *bias,
+                          int32_t *output, void *stream);
+
 /* ---- requantized int8 output (the step after the path) ---------------- */
 
 /* No counterpart in the reference: its vendor comparison writes INT8 output

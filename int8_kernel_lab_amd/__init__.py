@@ -37,7 +37,7 @@ __all__ = [
     "WORKLOADS_DIR", "BASELINE_SEED", "device_count", "device_info", "set_device",
     "synchronize", "requantize", "requant_fused", "requant_workspace_bytes", "launch_requant",
     "conv2d_requant", "measure_requant", "nchw_to_nhwc", "nhwc_to_nchw", "nhwk_to_nkhw",
-    "pack_vect_c", "unpack_vect_c", "measure_graph", "measure_store_floor", "wait_expired",
+    "pack_vect_c", "unpack_vect_c", "measure_graph", "measure_store_floor", "wait_expired", "launch_noalloc",
 ]
 
 KERNELS = ("generic", "strip", "halo", "splitk")
@@ -253,6 +253,19 @@ def launch(name: str, shape: ConvShape, input, filter, bias, output,
                                  _ptr(input), _ptr(filter), _ptr(bias), _ptr(output),
                                  _ptr(workspace), int(workspace_nbytes), _ptr(stream))
     check(status, f"launch {name}")
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20  # the static scratch of launch_noalloc (i8conv.h)
+
+
+def launch_noalloc(name: str, shape: ConvShape, input, filter, bias, output,
+                   stream=None) -> None:
+    """i8conv_launch_noalloc: kernel `name` with its workspace (if any) in
+    the library's static per-GPU scratch of 16 MiB; allocates nothing.
+    Calls that overlap in time on one GPU race on that scratch."""
+    check(lib().i8conv_launch_noalloc(_kernel_id(name), ctypes.byref(shape.c_struct()),
+                                      _ptr(input), _ptr(filter), _ptr(bias), _ptr(output),
+                                      _ptr(stream)), f"launch_noalloc {name}")
 
 
 def launch_generic(shape: ConvShape, input, filter, bias, output, stream=None) -> None:

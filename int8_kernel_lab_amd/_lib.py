@@ -67,6 +67,8 @@ SIGNATURES = {
     "i8conv_launch_spatial_strip": (c_int, [POINTER(CShape), c_void_p, c_void_p,
                                             c_void_p, c_void_p, c_void_p]),
     "i8conv_spatial_strip_eligible": (c_int, [POINTER(CShape)]),
+    "i8conv_launch_noalloc": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,
+                                      c_void_p, c_void_p]),
     "i8conv_launch_dispatched": (c_int, [POINTER(CShape), c_void_p, c_void_p, c_void_p,
                                          c_void_p, c_void_p, c_size_t, c_void_p]),
     "i8conv_requantize": (c_int, [c_void_p, c_int64, c_int32, c_void_p, c_void_p, c_int32,

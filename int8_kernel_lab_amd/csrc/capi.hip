@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <chrono>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -179,6 +180,47 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   }
   (void)hipStreamDestroy(s);
   return rc;
+}
+}  // namespace
+
+// Scratch of i8conv_launch_noalloc: a file-scope device array of
+// kScratchBytes, one copy per GPU (each GPU the library runs on holds it
+// until the process ends).  Host code never passes `scratch` itself to a
+// kernel (on the host the name is a stand-in, not a device address): it
+// uses the address hipGetSymbolAddress returns on each device, kept per
+// device in g_scratch_ptr.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+constexpr int kScratchDevices = 64;
+__device__ __attribute__((aligned(256))) int32_t scratch[kScratchBytes / sizeof(int32_t)];
+
+namespace {
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kScratchDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with
+// that device current) and then reused.
+int scratch_for_current_device(void **ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail("hipGetDevice", e);
+  if (dev < 0 || dev >= kScratchDevices) {
+    set_error("launch_noalloc: device index " + std::to_string(dev) + " beyond the " +
+              std::to_string(kScratchDevices) + " devices the scratch table covers");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail("hipGetSymbolAddress(scratch)", e);
+    if (!p) {
+      set_error("hipGetSymbolAddress(scratch) returned a null address");
+      return I8CONV_HIP_ERROR;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return I8CONV_OK;
 }
 }  // namespace
 
@@ -387,6 +429,26 @@ int i8conv_launch_dispatched(const i8conv_shape *shape, const int8_t *input,
   }
   return i8conv_launch(id, shape, input, filter, bias, output, workspace,
                        workspace_bytes, stream);
+}
+
+int i8conv_launch_noalloc(int id, const i8conv_shape *shape, const int8_t *input,
+                          const int8_t *filter, const int32_t *bias, int32_t *output,
+                          void *stream) {
+  // 0 for kernels without a workspace, and for an unknown id, a bad shape
+  // or an ineligible one: i8conv_launch then reports those
+  const size_t need = i8conv_workspace_bytes(id, shape);
+  if (need > kScratchBytes) {
+    set_error("launch_noalloc: " + std::string(i8conv_kernel_name(id)) + " needs " +
+              std::to_string(need) + " bytes of scratch for this shape; the library's static "
+              "scratch holds " + std::to_string(kScratchBytes) +
+              " (pass a workspace to i8conv_launch instead)");
+    return I8CONV_WORKSPACE_TOO_SMALL;
+  }
+  void *ws = nullptr;
+  if (need > 0) {
+    if (const int rc = scratch_for_current_device(&ws); rc != I8CONV_OK) return rc;
+  }
+  return i8conv_launch(id, shape, input, filter, bias, output, ws, need, stream);
 }
 
 // ---- requantized int8 output -------------------------------------------------
