@@ -15,12 +15,24 @@
 // consume them, in chunks: padded input row r (both 64-channel groups),
 // preceded for r <= 2 by the taps of filter row r (input row r feeds output
 // rows r - fy, so filter row r is first needed at input row r), the bias
-// first of all.  Each copy wave signals a chunk through an LDS counter once
-// its copies of it have landed; the MFMA waves walk the input rows, wait for
-// each row's chunk just before reading it, and store output row o once it
-// is complete (one row after input row o + 2).  The MFMAs start after the
-// first chunk (~9 KB) instead of all the copies, and the stores are spread
-// over the walk.  With 4 fragments per row the registers do not hold both
+// first of all.  Each copy wave follows each chunk with a flag copy (below)
+// and never waits; the MFMA waves walk the input rows, wait for each row's
+// chunk just before reading it, and store output row o once it is complete
+// (one row after input row o + 2).  The MFMAs start after the first chunk
+// (~9 KB) instead of all the copies, and the stores are spread over the
+// walk.
+//
+// Flags.  A copy wave's loads return in the order it issued them (the
+// property that makes vmcnt a count of the oldest loads outstanding), and
+// an LDS-DMA load writes LDS when it returns.  So after issuing its copies
+// of chunk c a copy wave issues one more: a 4-byte LDS-DMA copy, from lane
+// 0 only (the copy writes only the active lanes), of a device word holding
+// 1 into its flag word of chunk c.  Once that flag reads 1, all of the
+// wave's copies of chunk c are in LDS.  The copy waves thus issue all their
+// copies without a single wait: a wave that waits for chunk c before
+// signalling it (vmcnt, then an LDS add) cannot issue meanwhile, and the
+// compute unit's loads in flight drop (28x28x128: 6.44 -> 6.14 us per
+// launch, same box).  With 4 fragments per row the registers do not hold both
 // groups: the walk then runs twice, group 0 (accumulating every output row
 // of the block) and group 1 (completing and storing them).
 //
@@ -79,9 +91,8 @@ struct PassArgs {
   FastDiv3 div_plane_copies, div_hp, div_blocks, div_tiles_n;
 };
 
-// Cross-wave signals in LDS: a copy wave adds 1 to a chunk's counter once
-// its copies of that chunk have landed (its own vmcnt says so: LDS-DMA data
-// is in LDS when the count drops), and the MFMA waves poll the counter.
+// Cross-wave signals in LDS: flag words set by LDS-DMA flag copies behind
+// each chunk (see the top of this file), polled by the MFMA waves.
 // The wait is bounded: after kSpinLimit polls (each a read and a sleep of
 // about 64 cycles, some tens of ms in all, far beyond any real copy time) it
 // gives up, so that every wave always reaches the end of the kernel.  A
@@ -91,30 +102,35 @@ struct PassArgs {
 // after synchronizing, and must treat the output of the launches since the
 // last check as wrong when it is set.
 constexpr int kSpinLimit = 1 << 20;
-constexpr int kCopyWaves = 4;
 
-// Adds 1 to the counter at LDS address addr (no wait: the wave waits for
-// its LDS operations once, before it ends).
-__device__ __forceinline__ void flag_add(uint32_t addr) {
-  asm volatile("ds_add_u32 %0, %1" ::"v"(addr), "v"(1) : "memory");
+// The source word of every flag copy.
+__device__ __attribute__((aligned(16))) int g_flag_one[4] = {1, 1, 1, 1};
+
+// A compiler-visible read of the four flag words (one per copy wave) of a
+// chunk at LDS address addr, issued ahead of its use: the compiler waits
+// for it where the value is tested, a row later.
+__device__ __forceinline__ v4i flag_peek(uint32_t addr) {
+  return *reinterpret_cast<volatile __attribute__((address_space(3))) v4i *>(size_t(addr));
 }
 
-// A compiler-visible read of the counter at LDS address addr, issued ahead
-// of its use (the compiler waits for it where the value is needed).
-__device__ __forceinline__ int flag_peek(uint32_t addr) {
-  return *reinterpret_cast<volatile __attribute__((address_space(3))) int *>(size_t(addr));
+// All four copy waves' copies of the chunk have landed (wave-uniform).
+__device__ __forceinline__ bool flags_set(v4i f) {
+  return __builtin_amdgcn_readfirstlane(f[0] & f[1] & f[2] & f[3]) != 0;
 }
 
-__device__ __forceinline__ void flag_wait(uint32_t addr, int target) {
+__device__ __forceinline__ void flag_wait(uint32_t addr) {
   for (int spin = 0; spin < kSpinLimit; ++spin) {
-    int v;
-    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
-    if (__builtin_amdgcn_readfirstlane(v) >= target) return;
+    v4i v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+    if (flags_set(v)) return;
     __builtin_amdgcn_s_sleep(1);
   }
-  // the chunk never arrived: every lane stores the same word (one vector
-  // store), the host finds it set after the launch
-  *reinterpret_cast<volatile unsigned int *>(&g_wait_expired) = 1u;
+  // the chunk never arrived: every lane stores the same word (one global
+  // vector store, agent scope), the host finds it set after the launch.  A
+  // relaxed atomic store is a plain global store; a volatile one through a
+  // generic pointer was a flat store plus a wait for all memory operations,
+  // which the compiler then also assumed after every wait.
+  __hip_atomic_store(&g_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // State of one wave's row walk over output rows [OLO, OHI) of the block
@@ -131,8 +147,8 @@ struct PassState {
   const int8_t *halves;    // this wave's filter halves: (group, tap) 1 KB each
   const int8_t *bias_lds;  // this wave's 16 bias values
   int plane_bytes;
-  uint32_t counters;       // LDS address of the chunk counters
-  int peeked;              // counter of the next row's chunk, read one row ahead
+  uint32_t flags;          // LDS address of the chunk flags: 16 bytes per chunk
+  v4i peeked;              // flags of the next row's chunk, read one row ahead
   // Output, vector path: a buffer resource over y, this lane's byte offset
   // of output row 0 per fragment (out of range where the column or the
   // channels fall outside the layer: the store is dropped, no branch), and
@@ -186,7 +202,7 @@ struct PassState {
   // order the copy waves issue them (group-major when NG == 1).
   template <int G>
   __device__ __forceinline__ uint32_t counter(const PassArgs &p, int r) const {
-    return counters + 4u * uint32_t((G / NG) * p.rows_in + r);
+    return flags + 16u * uint32_t((G / NG) * p.rows_in + r);
   }
 
   template <int G, int FY>
@@ -204,7 +220,7 @@ struct PassState {
   // row's taps: input row OLO + t first needs filter row t) are read,
   // interleaved with the MFMAs of this row into output rows IR - fy
   // (compile-time valid ones); in the last walk, output row IR - 3 is then
-  // stored.  The counter of the chunk after next is read here and checked
+  // stored.  The flags of the chunk after next are read here and tested
   // one row later, so a chunk that has landed costs no wait.
   template <int G, int IR>
   __device__ __forceinline__ void step(const PassArgs &p, bool vec, int rows_out, int m_row0,
@@ -217,13 +233,13 @@ struct PassState {
 #pragma unroll
         for (int j = 0; j < NFR; ++j) cur[g][fx][j] = frag[g][fx][j];
     if (IR + 1 < OHI + 2) {
-      const int seen = peeked;
+      const v4i seen = peeked;
       if (IR + 2 < OHI + 2) peeked = flag_peek(counter<G>(p, IR + 2));
-      if (seen < kCopyWaves) flag_wait(counter<G>(p, IR + 1), kCopyWaves);
+      if (!flags_set(seen)) flag_wait(counter<G>(p, IR + 1));
       // keeps the compiler from moving the plain LDS reads of load_row (and
-      // take_taps) above the counter check on the path that skips
-      // flag_wait (whose asm already orders them); the hardware issues a
-      // wave's LDS operations in order, so no wait instruction is needed
+      // take_taps) above the flag test on the path that skips flag_wait
+      // (whose asm already orders them); the hardware issues a wave's LDS
+      // operations in order, so no wait instruction is needed
       asm volatile("" ::: "memory");
       constexpr int fy_next = IR + 1 - OLO;
       if (fy_next <= 2) take_taps<G, (fy_next <= 2 ? fy_next : 0)>(lane);
@@ -319,7 +335,7 @@ struct PassState {
   template <int G, size_t... I>
   __device__ __forceinline__ void walk(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                        int oc0, int lane, std::index_sequence<I...>) {
-    flag_wait(counter<G>(p, OLO), kCopyWaves);
+    flag_wait(counter<G>(p, OLO));
     peeked = flag_peek(counter<G>(p, OLO + 1));
     take_taps<G, 0>(lane);
     load_row<G>(p, OLO);
@@ -341,64 +357,30 @@ struct PassState {
 // r <= 2 by the filter taps of filter row r (the first row an input row
 // needs them at: input row r feeds output rows r - fy), and the bias first
 // of all.  Copy wave w copies MFMA wave w's filter halves and plane copies
-// j = w + 4i of every row.  A copy wave signals chunk c (adds 1 to its
-// counter) once its copies of c have landed, and the MFMA waves wait for
-// each row's chunk just before reading it: the MFMAs start after the first
-// chunk instead of half or all of the copies.
-constexpr int kSignalLag = 4;
-
+// j = w + 4i of every row, then its flag copy of the chunk, and never
+// waits; the MFMA waves wait for each row's chunk just before reading it:
+// the MFMAs start after the first chunk instead of half or all of the
+// copies.
+//
 // The copy waves' schedule, unrolled at compile time (R + 2 padded input
 // rows per walk, NG groups per chunk, PW plane copies per row and group
-// from this wave): chunk k is issued in order, and chunk c is signalled
-// right after issuing the first chunk k that puts kSignalLag or more of this
-// wave's copies after c (vmcnt(after) then covers c), or after vmcnt(0) at
-// the end.  Straight-line code: a copy wave's scalar work per chunk is a
-// few instructions, so its issue keeps up with the copies (a loop with a
-// run-time vmcnt switch per chunk was several times slower).
+// from this wave): chunk k's copies, then its flag, in order.  Straight-
+// line code: a copy wave's scalar work per chunk is a few instructions, so
+// its issue keeps up with the copies.  The wave waits for all of its loads
+// once, at the end (before it ends, or walks rows itself).
 template <int R, int PW, int NG>
 struct CopySchedule {
   static constexpr int kRows = R + 2;
   static constexpr int kChunks = (kGroups / NG) * kRows;
-  static constexpr int copies(int k) {
-    return (k == 0 ? 1 : 0) + (k % kRows <= 2 ? 3 * NG : 0) + NG * PW;
-  }
-  static constexpr int after(int c, int k) {
-    int n = 0;
-    for (int i = c + 1; i <= k; ++i) n += copies(i);
-    return n;
-  }
-  static constexpr int signal_at(int c) {
-    for (int k = c; k < kChunks; ++k)
-      if (after(c, k) >= kSignalLag) return k;
-    return kChunks;
-  }
-
-  template <int K, int C, class Signal>
-  __device__ static __forceinline__ void maybe_signal(Signal &signal) {
-    if constexpr (signal_at(C) == K) {
-      if constexpr (K < kChunks) {
-        constexpr int n = after(C, K) < 63 ? after(C, K) : 63;
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-      }
-      signal(C);
-    }
-  }
-  template <int K, class Signal, size_t... C>
-  __device__ static __forceinline__ void signals(Signal &signal, std::index_sequence<C...>) {
-    (maybe_signal<K, int(C)>(signal), ...);
-  }
   template <class Issue, class Signal, size_t... K>
   __device__ static __forceinline__ void steps(Issue &issue, Signal &signal,
                                                std::index_sequence<K...>) {
-    ((issue((int(K) / kRows) * NG, int(K) % kRows, PW, NG),
-      signals<int(K)>(signal, std::make_index_sequence<kChunks>{})),
-     ...);
+    ((issue((int(K) / kRows) * NG, int(K) % kRows, PW, NG), signal(int(K))), ...);
   }
   template <class Issue, class Signal>
   __device__ static __forceinline__ void run(Issue &issue, Signal &signal) {
     steps(issue, signal, std::make_index_sequence<kChunks>{});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    signals<kChunks>(signal, std::make_index_sequence<kChunks>{});
   }
 };
 
@@ -413,7 +395,7 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
   st.plane_bytes = p.plane_copies * 1024;
   const int8_t *ring = st.planes + kGroups * p.rows_in * st.plane_bytes;
   st.halves = ring + wave * kHalves * 1024;
-  st.counters = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
+  st.flags = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
 #pragma unroll
   for (int fx = 0; fx < 3; ++fx)
 #pragma unroll
@@ -500,19 +482,19 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   const int tile_n = tn * 64;
 
   // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows]
-  //      [filter halves: 18 KB per wave][chunk counters]
+  //      [filter halves: 18 KB per wave][chunk flags: 16 B per chunk]
   const int8_t *bias_lds = smem + wave * 256;
   const int8_t *planes = smem + kHaloBiasLds;
   const int plane_bytes = p.plane_copies * 1024;
   const int8_t *ring = planes + kGroups * p.rows_in * plane_bytes;
   const int8_t *halves = ring + wave * kHalves * 1024;
-  const uint32_t counters = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
+  const uint32_t flags = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
   const int nchunks = (kGroups / NG) * p.rows_in;
   constexpr int kSplit = split_rows(R, NG, kQ);
 
   if (wave_id == 0 && lane < nchunks) {
-    // every counter starts at zero before any wave adds to it
-    asm volatile("ds_write_b32 %0, %1" ::"v"(counters + 4u * uint32_t(lane)), "v"(0)
+    // every flag starts at zero before any copy can land
+    asm volatile("ds_write_b128 %0, %1" ::"v"(flags + 16u * uint32_t(lane)), "v"(v4i{0, 0, 0, 0})
                  : "memory");
   }
   __syncthreads();
@@ -566,8 +548,11 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
         }
       }
     };
+    // the flag copy of chunk c: lane 0 copies the word holding 1 into this
+    // wave's flag word of the chunk (the other lanes are inactive)
+    const v4u one = make_desc(g_flag_one, 16u);
     auto signal = [&](int c) {
-      if (lane == 0) flag_add(counters + 4u * uint32_t(c));
+      if (lane == 0) lds_copy4(one, flags + 16u * uint32_t(c) + 4u * uint32_t(wave), 0u);
     };
     // plane copies per row and group this wave issues: j = wave, wave + 4
     const int pw = p.plane_copies > wave ? (p.plane_copies - wave + 3) / 4 : 0;
@@ -576,8 +561,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     else CopySchedule<R, 2, NG>::run(issue_chunk, signal);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // With a split, the copy wave then walks the block's last rows for its
-    // MFMA wave's 16 channels (its copies have landed; the chunk counters
-    // say when the other copy waves' have).
+    // MFMA wave's 16 channels (its copies have landed; the chunk flags say
+    // when the other copy waves' have).
     if constexpr (kSplit > 0)
       run_walk<R, NFR, NG, kQ, kSplit, R>(p, smem, wave, lane, b, oy0, rows_out, tile_n);
     return;
@@ -630,7 +615,7 @@ int rowpass_max_rows(int nfr) { return nfr == 4 ? 4 : 8; }
 size_t rowpass_lds_bytes(int wp, int rows) {
   const size_t plane_copies = (size_t(wp) * kUnits + 63) / 64;
   return size_t(kHaloBiasLds) + size_t(kGroups) * size_t(rows + 2) * plane_copies * 1024 +
-         size_t(4) * kHalves * 1024 + 128;  // + chunk counters (2 x up to 10 rows)
+         size_t(4) * kHalves * 1024 + 512;  // + chunk flags (16 B x 2 x up to 10 rows)
 }
 
 int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream, const RequantArgs *q) {
