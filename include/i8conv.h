@@ -269,9 +269,14 @@ typedef struct i8conv_graph_timing {
  *   4. warmup: main-graph replays until at least `warmup` launches have run
  *      and at least min_warmup_ms of host wall time has passed;
  *   5. the output is poisoned again (step 2), so that it then holds only
- *      what the timed replays wrote;
- *   6. timed region: iterations / L main-graph replays plus the remainder
- *      graph, exactly `iterations` launches, between one event pair.
+ *      what graph replays wrote;
+ *   6. one more main-graph replay, untimed and not waited for, so that the
+ *      timed launches start behind running ones;
+ *   7. timed region: iterations / L main-graph replays plus the remainder
+ *      graph, exactly `iterations` launches, between one pair of events
+ *      recorded on the stream.  Each graph replay begins with a gap of some
+ *      microseconds after the previous one, which the timed region holds
+ *      once per replay: a larger L spreads it over more launches.
  * Fills *timing.  Synchronous. */
 int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
                          const int8_t *filter, const int32_t *bias, int32_t *output,

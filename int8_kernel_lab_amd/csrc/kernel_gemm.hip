@@ -205,8 +205,8 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_vec(
     int32_t *__restrict__ y, int n4, size_t total4, int splits) {
   // Each thread walks vec4 items q, q + G, ... (G threads in the grid); its
   // channel group q mod n4 is found once and then advanced by G mod n4,
-  // so the loop has no 64-bit division.  The splits are added eight loads
-  // at a time (all in flight together), still in split order.
+  // so the loop has no 64-bit division.  The splits are added sixteen
+  // loads at a time (all in flight together), still in split order.
   // The stores go through a window over the workgroup's kThreads items of
   // the pass (base qb, uniform), so 16-byte offsets stay small.
   const size_t grid = size_t(gridDim.x) * kThreads;
@@ -218,12 +218,19 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_vec(
       const v4i *src = reinterpret_cast<const v4i *>(partial) + q;
       v4i acc = reinterpret_cast<const v4i *>(bias)[c4];
       int sp = 0;
-      for (; sp + 8 <= splits; sp += 8) {
-        v4i t[8];
+      for (; sp + 16 <= splits; sp += 16) {
+        v4i t[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) t[u] = src[size_t(sp + u) * total4];
+        for (int u = 0; u < 16; ++u) t[u] = src[size_t(sp + u) * total4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = add_wrap(acc, t[u]);
+        for (int u = 0; u < 16; ++u) acc = add_wrap(acc, t[u]);
+      }
+      for (; sp + 4 <= splits; sp += 4) {
+        v4i t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = src[size_t(sp + u) * total4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = add_wrap(acc, t[u]);
       }
       for (; sp < splits; ++sp) acc = add_wrap(acc, src[size_t(sp) * total4]);
       const auto y_r = make_rsrc(reinterpret_cast<v4i *>(y) + qb,

@@ -28,10 +28,12 @@
 //     that also issues copies stalls whenever the buffer unit's queue is
 //     full, and its MFMAs wait behind the stalled issue;
 //   * accumulators stay in VGPRs (built with -amdgpu-mfma-vgpr-form);
-//   * XCD-aware tile order (see below).
+//   * XCD-aware tile order (see below);
+//   * fragments wholly past the last pixel row run no MFMAs.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "i8conv_internal.hpp"
 
@@ -45,6 +47,20 @@ typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v4i add_wrap(v4i a, v4i b) {
   // int32 addition with two's-complement wrap, like the MFMA accumulator.
   return __builtin_bit_cast(v4i, __builtin_bit_cast(v4u_t, a) + __builtin_bit_cast(v4u_t, b));
+}
+
+// Calls run(std::integral_constant<int, F>) with F = min(live, FMAX).
+template <int F, int FMAX, class Run>
+__device__ __forceinline__ void with_live_frags(int live, Run &run) {
+  if constexpr (F < FMAX) {
+    if (live <= F) {
+      run(std::integral_constant<int, F>{});
+      return;
+    }
+    with_live_frags<F + 1, FMAX>(live, run);
+  } else {
+    run(std::integral_constant<int, FMAX>{});
+  }
 }
 
 // NCW == 0: every wave both copies and runs MFMAs.  NCW > 0: WM*WN MFMA
@@ -209,25 +225,35 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
     for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
   if (NCW > 0) {
-    // MFMA wave of a split workgroup: the copy waves fill the ring
-    for (int st = s_begin; st < s_end; ++st) {
-      __syncthreads();
-      const int8_t *buf = smem + ((st - s_begin) % kRing) * kTile;
-      v4i af[2][FN], bf[2][FM];
+    // MFMA wave of a split workgroup: the copy waves fill the ring.  The
+    // wave's fragments that lie wholly at or past m_end (the padding of a
+    // last pixel tile: 120 of the 128 rows of the deep-K layer's fourth)
+    // get no fragment reads and no MFMAs: the walk runs with the live
+    // fragment count as a compile-time constant.
+    const int row0 = tile_m + wm * TMW;
+    const int live = m_end <= row0 ? 0 : min(FM, (m_end - row0 + 15) / 16);
+    auto walk = [&](auto live_frags) {
+      constexpr int F = decltype(live_frags)::value;
+      for (int st = s_begin; st < s_end; ++st) {
+        __syncthreads();
+        const int8_t *buf = smem + ((st - s_begin) % kRing) * kTile;
+        v4i af[2][FN], bf[2][F > 0 ? F : 1];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int i = 0; i < FN; ++i) af[h][i] = *reinterpret_cast<const v4i *>(buf + aoff[h][i]);
+          for (int i = 0; i < FN; ++i) af[h][i] = *reinterpret_cast<const v4i *>(buf + aoff[h][i]);
 #pragma unroll
-        for (int j = 0; j < FM; ++j) bf[h][j] = *reinterpret_cast<const v4i *>(buf + boff[h][j]);
+          for (int j = 0; j < F; ++j) bf[h][j] = *reinterpret_cast<const v4i *>(buf + boff[h][j]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < F; ++j) acc[i][j] = mfma16(af[h][i], bf[h][j], acc[i][j]);
       }
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < FN; ++i)
-#pragma unroll
-          for (int j = 0; j < FM; ++j) acc[i][j] = mfma16(af[h][i], bf[h][j], acc[i][j]);
-    }
+    };
+    with_live_frags<0, FM>(live, walk);
   }
   if (NCW == 0) issue(s_begin);
   if (NCW == 0 && s_begin + 1 < s_end) issue(s_begin + 1);

@@ -237,8 +237,9 @@ def test_graph_replays_bit_exact(case, baseline_cases):
     # the bench's timing path: launches captured in HIP graphs (split-K: two
     # kernels per launch, the workspace rewritten every launch); the output
     # is poisoned outside the graphs right before the timed replays, so the
-    # check sees only what the replays wrote.  Two calls: a main graph that
-    # divides the launches, then one with a remainder graph (7 = 2 x 3 + 1).
+    # check sees only what the replays wrote.  Three calls: a main graph that
+    # divides the launches, one with a remainder graph (7 = 2 x 3 + 1), and
+    # one graph holding every timed launch (the bench's form).
     shape = baseline_cases[case]
     kernel = lab.dispatch(shape)
     x, w, b, expected = _case(case, shape)
@@ -248,7 +249,7 @@ def test_graph_replays_bit_exact(case, baseline_cases):
     ws_n = lab.workspace_bytes(kernel, shape)
     ws = lab.DeviceBuffer(ws_n) if ws_n else None
     try:
-        for call, (iterations, per_graph) in enumerate([(6, 3), (7, 3)]):
+        for call, (iterations, per_graph) in enumerate([(6, 3), (7, 3), (5, 5)]):
             say(f"[gpu] graph replays {kernel} on {case}, call {call}")
             t = lab.measure_graph(kernel, shape, *bufs, yb, ws, ws_n, warmup=2,
                                   iterations=iterations, launches_per_graph=per_graph,
