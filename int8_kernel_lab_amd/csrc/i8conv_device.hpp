@@ -225,14 +225,21 @@ __device__ __forceinline__ v4i load_bias4(const int32_t *base, int count, int i0
 //    in the L2 and the release at the end of the kernel writes them back
 //    after the last wave has finished, which the next launch on the stream
 //    waits for (28x28x128 layer: 7.8 -> 7.1 us per launch; split-K on the
-//    deep-K layer 15.1 -> 14.6 us).
+//    deep-K layer 15.1 -> 14.6 us).  The pipelined GEMM uses it too, with
+//    each wave storing a pixel row's channel fragments back to back so that
+//    whole lines arrive together: the layers then write exactly their output
+//    bytes (stride-2 3x3 layer: 14.1 us; 15.5 us and 1.29x the output bytes
+//    with evict-first stores issued one channel fragment at a time).
 //  * kStoreStream, nt (bit 1): evict-first lines written back by the L2.
-//    For the pipelined GEMM, which stores a whole tile in one burst at its
-//    end: the L2 absorbs the burst faster than memory would (stride-2 3x3
-//    layer: 15.5 us, 16.7 us with write-through).  The output of a layer is
-//    several times larger than its input and filter and is written once, so
-//    evict-first keeps the input rows and filter in the L2.
+//    Partly written lines leave the L2 as partial writes, so it pays only
+//    where every store covers whole lines.
 // (sc1 and nt together made the K = 36 row-kernel layer 25 % slower.)
+// Write-through sends each store's bytes on at once, so the pieces must be
+// whole 32-byte memory sectors: a wave's 16-channel slice of a pixel (64
+// bytes) starts on a sector only when the pixel pitch N * 4 is a multiple of
+// 32.  Other channel counts store ordinarily, and the L2 merges the slices
+// into whole lines (K = 36 layer: 1.33x the output bytes written through,
+// 1.00x ordinary, 4.08 -> 4.13 us).
 // The 4-byte stores of a channel tail (N % 4 != 0) stay ordinary: each
 // covers a sliver of a line, and only ordinary stores are merged into whole
 // lines in the L2 (non-temporal ones went to HBM as partial writes and made
@@ -244,6 +251,11 @@ template <int kPolicy>
 __device__ __forceinline__ void store_out4(__amdgpu_buffer_rsrc_t out, uint32_t byte_off, v4i v) {
   __builtin_amdgcn_raw_buffer_store_b128(v, out, byte_off, 0, kPolicy);
 }
+
+// Write-through for sector-aligned pixel pitches (N % 8 == 0), else ordinary.
+// Kernels pick the policy once per launch or per epilogue, not per store: a
+// per-store branch cost 2-4 % on the GEMM layers.
+__device__ __forceinline__ bool sector_pitch(int gemm_n) { return (gemm_n & 7) == 0; }
 
 // A workgroup's output window: a buffer resource over pixels (GEMM rows)
 // [m0, m0 + rows) of an [M][N] int32 tensor, clamped to M, so that

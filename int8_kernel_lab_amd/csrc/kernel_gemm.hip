@@ -17,6 +17,8 @@
 //     order plus the bias (deterministic; integer addition is exact).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "i8conv_internal.hpp"
 
 namespace i8conv {
@@ -171,31 +173,44 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(ConvArgs a) {
   if (kSplit) out = a.partial + size_t(blockIdx.y) * size_t(a.gemm_m) * size_t(a.gemm_n);
   const OutWindow ow = out_window(out, a.gemm_m, a.gemm_n, tile_m, BM);
   const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ow.ok;
+  // a pixel's channel fragments back to back, as in kernel_gemm_dma.hip
+  v4i bias[FN];
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
-    v4i bv = v4i{0, 0, 0, 0};
+    bias[i] = v4i{0, 0, 0, 0};
     if (!kSplit) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (oc0 + e < a.gemm_n) bv[e] = a.bias[oc0 + e];
+        if (oc0 + e < a.gemm_n) bias[i][e] = a.bias[oc0 + e];
     }
+  }
+  auto store_tile = [&](auto policy) {
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
       if (px >= a.gemm_m) continue;
-      const v4i v = add_wrap(acc[i][j], bv);
-      if (vec) {
-        if (oc0 < a.gemm_n)
-          store_out4<kSplit ? kStoreThrough : kStoreStream>(ow.r, (uint32_t(px - tile_m) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
-      } else {
-        int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (oc0 + e < a.gemm_n) dst[e] = v[e];
+      for (int i = 0; i < FN; ++i) {
+        const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
+        const v4i v = add_wrap(acc[i][j], bias[i]);
+        if (vec) {
+          if (oc0 < a.gemm_n)
+            store_out4<decltype(policy)::value>(
+                ow.r, (uint32_t(px - tile_m) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
+        } else {
+          int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (oc0 + e < a.gemm_n) dst[e] = v[e];
+        }
       }
     }
-  }
+  };
+  if (sector_pitch(a.gemm_n))
+    store_tile(std::integral_constant<int, kStoreThrough>{});
+  else
+    store_tile(std::integral_constant<int, 0>{});
 }
 
 // Second pass of split-K: y = bias + partial[0] + partial[1] + ... in split

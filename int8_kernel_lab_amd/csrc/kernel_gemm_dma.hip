@@ -297,30 +297,48 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
   }
 
   // Epilogue: lane holds channels oc0..oc0+3 of pixel px for each fragment.
+  // The channel fragments of one pixel fragment are stored back to back
+  // (i innermost), so the wave's 16-channel slices of a pixel row, 64 bytes
+  // each, reach the L2 together and fill whole 128-byte lines; written
+  // through (sector-aligned pitches) the layer then writes exactly its
+  // output bytes.
   int32_t *out = a.y;
   if (kSplit) out = a.partial + size_t(blockIdx.y) * size_t(a.gemm_m) * size_t(a.gemm_n);
   const OutWindow ow = out_window(out, a.gemm_m, a.gemm_n, tile_m, a.m_step);
   const bool vec = (a.gemm_n & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 && ow.ok;
+  v4i bias[FN];
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
-    const v4i bv = kSplit ? v4i{0, 0, 0, 0} : load_bias4(a.bias, a.gemm_n, oc0);
+    bias[i] = kSplit ? v4i{0, 0, 0, 0} : load_bias4(a.bias, a.gemm_n, oc0);
+  }
+  auto store_tile = [&](auto policy) {
 #pragma unroll
     for (int j = 0; j < FM; ++j) {
       const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
       if (px >= m_end) continue;
-      const v4i v = add_wrap(acc[i][j], bv);
-      if (vec) {
-        if (oc0 < a.gemm_n)
-          store_out4<kSplit ? kStoreThrough : kStoreStream>(ow.r, (uint32_t(px - tile_m) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
-      } else {
-        int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (oc0 + e < a.gemm_n) store_out1(dst + e, v[e]);
+      for (int i = 0; i < FN; ++i) {
+        const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
+        const v4i v = add_wrap(acc[i][j], bias[i]);
+        if (vec) {
+          if (oc0 < a.gemm_n)
+            store_out4<decltype(policy)::value>(
+                ow.r, (uint32_t(px - tile_m) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
+        } else {
+          int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (oc0 + e < a.gemm_n) store_out1(dst + e, v[e]);
+        }
       }
     }
-  }
+  };
+  // one uniform branch for the whole epilogue
+  if (sector_pitch(a.gemm_n))
+    store_tile(std::integral_constant<int, kStoreThrough>{});
+  else
+    store_tile(std::integral_constant<int, 0>{});
 }
 
 template <int BM, int BN, int WM, int WN, int NCW = 0>

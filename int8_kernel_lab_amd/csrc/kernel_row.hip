@@ -80,7 +80,7 @@ struct RowState {
 // the MFMAs of the previous one, so with one wave per SIMD the LDS latency
 // is hidden behind MFMAs instead of stalling them.  The last input row (only
 // filter row 2 left: MASK 4, or 7 in a one-row block) reads row 0 again.
-template <int FN, int CG, int NFR, int K, int MASK, bool kCheck>
+template <int FN, int CG, int NFR, int kPolicy, int K, int MASK, bool kCheck>
 __device__ __forceinline__ void row_step(const RowArgs &p, RowState<FN, CG, NFR> &st,
                                          v4i (&frag)[3][NFR], const int8_t *rows,
                                          const int8_t *bias_lds, int ir, int rows_out,
@@ -157,7 +157,7 @@ __device__ __forceinline__ void row_step(const RowArgs &p, RowState<FN, CG, NFR>
       const v4i v = add_wrap4(st.acc[s2][j][i], bv[i]);
       if (vec) {
         if (oc0 < p.gemm_n)
-          store_out4<kStoreThrough>(ow.r, (uint32_t(col) * uint32_t(p.gemm_n) + uint32_t(oc0)) * 4u, v);
+          store_out4<kPolicy>(ow.r, (uint32_t(col) * uint32_t(p.gemm_n) + uint32_t(oc0)) * 4u, v);
       } else {
         int32_t *dst = p.y + size_t(m_row + col) * size_t(p.gemm_n) + oc0;
 #pragma unroll
@@ -176,7 +176,9 @@ __device__ __forceinline__ void take_chunks(FilterRing<FN, 9 * CG> &ring,
   for (int c = C0; c < C1; ++c) ring.take(c, st.wf);
 }
 
-template <int FN, int CG, int NFR>
+// kPolicy: the output store policy, write-through where the pixel pitch is
+// sector-aligned (sector_pitch), else ordinary.
+template <int FN, int CG, int NFR, int kPolicy>
 __global__ __launch_bounds__(kThreads, 1) void row_kernel(RowArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
   const RowArgs p = p_arg;
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(kThreads, 1) void row_kernel(RowArgs p_arg) {
   // taking chunk 0 also publishes the input rows (its barrier).
   constexpr int kC1 = (3 * CG + 1) / 2, kC2 = (6 * CG + 1) / 2;
 #define I8_ROW(K, MASK, CHECK, IR)                                                         \
-  row_step<FN, CG, NFR, K, MASK, CHECK>(p, st, frag, rows, bias_lds, IR, rows_out, m_row0, \
+  row_step<FN, CG, NFR, kPolicy, K, MASK, CHECK>(p, st, frag, rows, bias_lds, IR, rows_out, m_row0, \
                                         tile_n, wave, lane)
   take_chunks<FN, CG, NFR, 0, kC1>(ring, st);
   v4i frag[3][NFR];
@@ -286,7 +288,8 @@ __global__ __launch_bounds__(kThreads, 1) void row_kernel(RowArgs p_arg) {
 
 template <int FN, int CG, int NFR>
 int launch_t(const RowArgs &h, size_t blocks, size_t lds, hipStream_t s) {
-  auto kern = row_kernel<FN, CG, NFR>;
+  auto kern = (h.gemm_n & 7) == 0 ? row_kernel<FN, CG, NFR, kStoreThrough>
+                                  : row_kernel<FN, CG, NFR, 0>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
