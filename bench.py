@@ -154,6 +154,36 @@ def write_floor(workload: str, steps: int, warmup: int, min_warmup_ms: float) ->
     return 0
 
 
+def lds_probe(steps: int, warmup: int, min_warmup_ms: float) -> int:
+    """The LDS read probe in each pattern (i8conv_measure_lds_probe): 256
+    workgroups x 512 threads, 4097 16-byte reads per lane, timed like the
+    headline, each thread's XOR checked against the host's restatement.
+    Prints the time per launch and the LDS read rate per compute unit at the
+    2.4 GHz peak clock; under rocprofv3 --pmc the same launches give the
+    bank-conflict counters of a known pattern."""
+    import numpy as np
+    import int8_kernel_lab_amd as lab
+    workgroups, threads, reads = 256, 512, 4097
+    sink = lab.DeviceBuffer(4 * workgroups * threads)
+    out = {"lds_probe_workgroups": workgroups, "threads": threads, "reads_per_lane": reads,
+           "bytes_per_launch": 16 * reads * workgroups * threads, "launches": steps}
+    for pattern in lab.LDS_PROBE_PATTERNS:
+        t = lab.measure_lds_probe(pattern, sink, workgroups, threads, reads, warmup=warmup,
+                                  min_warmup_ms=min_warmup_ms, iterations=steps,
+                                  launches_per_graph=min(steps, 100))
+        got = sink.download(np.int32, workgroups * threads).reshape(workgroups, threads)
+        if not (got == lab.lds_probe_expected(pattern, threads, reads)[None, :]).all():
+            print(f"bench.py: the LDS probe ({pattern}) stored wrong values", file=sys.stderr)
+            return 1
+        us = t["mean_ms"] * 1e3
+        out[f"{pattern}_us_per_launch"] = round(us, 3)
+        out[f"{pattern}_bytes_per_clk_per_cu"] = round(
+            out["bytes_per_launch"] / (us * 1e-6) / 256 / 2.4e9, 1)
+    sink.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def requant_bench(workload: str, steps: int, warmup: int) -> int:
     """The same layer with requantized int8 output (i8conv_launch_requant:
     the dispatched kernel's fused epilogue where it has one, else the int32
@@ -235,6 +265,9 @@ def main() -> int:
                     help="instead of the benchmark, time the lab's store-only kernel writing "
                          "exactly the workload's int32 output bytes in the dispatched row "
                          "kernel's launch shape (and an empty kernel of that shape)")
+    ap.add_argument("--lds-probe", action="store_true",
+                    help="instead of the benchmark, time the LDS read probe in its four "
+                         "patterns (the control for the LDS bank-conflict counters)")
     ap.add_argument("--requant", action="store_true",
                     help="instead of the benchmark, time the same layer with requantized int8 "
                          "output (a separate line; the headline contract is int32 output)")
@@ -250,6 +283,8 @@ def main() -> int:
         return requant_bench(args.workload, args.steps, args.warmup)
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration, args.steps)
+    if args.lds_probe:
+        return lds_probe(args.steps, args.warmup, args.min_warmup_ms)
     if args.write_floor:
         return write_floor(args.workload, args.steps, args.warmup, args.min_warmup_ms)
 

@@ -37,7 +37,7 @@ __all__ = [
     "WORKLOADS_DIR", "BASELINE_SEED", "device_count", "device_info", "set_device",
     "synchronize", "requantize", "requant_fused", "requant_workspace_bytes", "launch_requant",
     "conv2d_requant", "measure_requant", "nchw_to_nhwc", "nhwc_to_nchw", "nhwk_to_nkhw",
-    "pack_vect_c", "unpack_vect_c", "measure_graph", "measure_store_floor", "wait_expired", "launch_noalloc",
+    "pack_vect_c", "unpack_vect_c", "measure_graph", "measure_store_floor", "measure_lds_probe", "wait_expired", "launch_noalloc",
 ]
 
 KERNELS = ("generic", "strip", "halo", "splitk")
@@ -353,6 +353,52 @@ def measure_store_floor(output, nbytes: int, workgroups: int = 256, threads: int
                                            int(launches_per_graph), ctypes.byref(t)),
           "measure_store_floor")
     return {f: getattr(t, f) for f, _ in _lib.CGraphTiming._fields_}
+
+
+LDS_PROBE_PATTERNS = ("linear", "swz128", "stride128", "stride256", "xor_rows", "pitch80")
+
+
+def measure_lds_probe(pattern: str, sink, workgroups: int = 256, threads: int = 512,
+                      reads_per_lane: int = 4097, warmup: int = 0, min_warmup_ms: float = 100.0,
+                      iterations: int = 200, launches_per_graph: int = 100) -> Dict[str, float]:
+    """Times the LDS read probe (i8conv_measure_lds_probe) in one of
+    LDS_PROBE_PATTERNS: ds_read_b128 only, the control pattern for the LDS
+    bank-conflict counters.  `sink` holds workgroups * threads int32."""
+    t = _lib.CGraphTiming()
+    check(lib().i8conv_measure_lds_probe(LDS_PROBE_PATTERNS.index(pattern), _ptr(sink),
+                                         int(workgroups), int(threads), int(reads_per_lane),
+                                         int(warmup), float(min_warmup_ms), int(iterations),
+                                         int(launches_per_graph), ctypes.byref(t)),
+          "measure_lds_probe")
+    return {f: getattr(t, f) for f, _ in _lib.CGraphTiming._fields_}
+
+
+def lds_probe_expected(pattern: str, threads: int, reads_per_lane: int):
+    """What thread t of any workgroup of the LDS probe stores (numpy int32
+    array of `threads` values): the per-lane offsets restated on the host."""
+    lane = np.arange(threads) % 64
+    row, chunk = lane % 16, lane // 16
+    if pattern == "linear":
+        base = 16 * lane
+    elif pattern == "swz128":
+        f = 2 * ((row + (row >> 2)) & 3) + ((row >> 2) & 1)
+        base = row * 128 + ((chunk ^ f) << 4)
+    elif pattern == "xor_rows":
+        base = row * 128 + ((chunk ^ (row & 7) ^ ((row >> 3) & 1)) << 4)
+    elif pattern == "pitch80":
+        base = 80 * row + 16 * chunk
+    elif pattern == "stride128":
+        base = 128 * lane
+    else:
+        base = 256 * lane
+    acc = np.zeros(threads, dtype=np.int64)
+    for shift in range(4):
+        # reads i with i % 4 == shift: (reads_per_lane - shift + 3) // 4 of them
+        if ((reads_per_lane - shift + 3) // 4) % 2 == 0:
+            continue
+        u = (base + 16384 * shift) // 16
+        acc ^= u ^ (~u) ^ (3 * u) ^ (u ^ 0x55)
+    return (acc & 0xFFFFFFFF).astype(np.uint32).view(np.int32)
 
 
 def wait_expired() -> bool:

@@ -106,6 +106,8 @@ SIGNATURES = {
     "i8conv_measure_store_floor": (c_int, [c_void_p, c_size_t, c_int, c_int, c_size_t, c_int,
                                            c_int, c_double, c_int, c_int,
                                            POINTER(CGraphTiming)]),
+    "i8conv_measure_lds_probe": (c_int, [c_int, c_void_p, c_int, c_int, c_int, c_int, c_double,
+                                         c_int, c_int, POINTER(CGraphTiming)]),
     "i8conv_measure": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,
                                c_void_p, c_void_p, c_size_t, c_void_p, c_int, c_int,
                                POINTER(c_float), POINTER(c_float)]),

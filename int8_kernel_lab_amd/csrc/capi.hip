@@ -306,7 +306,7 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
     else plan_halo(*shape, g, &p);
     if (p.row) {
       const size_t row_bytes =
-          size_t(halo_row_layout(shape->w + 2 * shape->pad_w, shape->c).row_bytes);
+          size_t(halo_row_layout(shape->w + 2 * shape->pad_w, shape->c, kRowPadUnits).row_bytes);
       const std::string lds =
           p.streamed ? std::to_string(rowpass_lds_bytes(shape->w + 2 * shape->pad_w, p.rows - 2) / 1024) +
                         " KB"
@@ -322,7 +322,7 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
           " pixel ranges of <=" + std::to_string(p.frags_m * 16) + "px x " +
           std::to_string(p.bn) + "oc, LDS " +
           std::to_string((kHaloBiasLds + size_t(p.rows) *
-                         size_t(halo_row_layout(shape->w + 2 * shape->pad_w, shape->c).row_bytes)) /
+                         size_t(halo_row_layout(shape->w + 2 * shape->pad_w, shape->c, kHaloPadUnits).row_bytes)) /
                          1024) + "+" +
           std::to_string(p.ring * halo_ring_slot_bytes(p.bn / 64) / 1024) + " KB, grid " +
           std::to_string(int64_t(p.ranges) * p.tiles_n);
@@ -765,6 +765,30 @@ int i8conv_measure_store_floor(int32_t *output, size_t bytes, int workgroups,
                                   write_through != 0, s);
       },
       output, bytes, warmup, min_warmup_ms, iterations, launches_per_graph, 0x5A, timing);
+}
+
+int i8conv_measure_lds_probe(int pattern, int32_t *sink, int workgroups,
+                             int threads_per_workgroup, int iterations_per_lane, int warmup,
+                             double min_warmup_ms, int iterations, int launches_per_graph,
+                             i8conv_graph_timing *timing) {
+  if (!sink || (reinterpret_cast<uintptr_t>(sink) & 3) != 0 || pattern < 0 || pattern > 5 ||
+      workgroups <= 0 || workgroups > (1 << 20) || threads_per_workgroup <= 0 ||
+      threads_per_workgroup > 1024 || threads_per_workgroup % 64 != 0 ||
+      iterations_per_lane <= 0 || warmup < 0 || !(min_warmup_ms >= 0.0) || iterations <= 0 ||
+      launches_per_graph <= 0 || !timing) {
+    set_error("measure_lds_probe needs a 4-byte aligned sink, pattern 0..5, 1..2^20 "
+              "workgroups of 64..1024 threads in whole waves, iterations_per_lane > 0, warmup "
+              ">= 0, min_warmup_ms >= 0, iterations and launches_per_graph > 0 and a timing "
+              "record");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  const size_t sink_bytes = size_t(workgroups) * size_t(threads_per_workgroup) * 4;
+  return measure_graph_loop(
+      [&](hipStream_t s) {
+        return launch_lds_probe(pattern, sink, workgroups, threads_per_workgroup,
+                                iterations_per_lane, s);
+      },
+      sink, sink_bytes, warmup, min_warmup_ms, iterations, launches_per_graph, 0x5A, timing);
 }
 
 int i8conv_measure_requant(const i8conv_shape *shape, const int8_t *input, const int8_t *filter,

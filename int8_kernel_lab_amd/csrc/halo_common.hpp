@@ -70,7 +70,7 @@ struct FilterRing {
     for (int j = 0; j < kCopies; ++j) {
       const int slot = (kCopies * wave + j) * 64 + lane;  // rows 16*FN*wave + [0, 16*FN)
       const int r = slot >> 3;
-      const int chunk16 = (slot & 7) ^ (r & 7) ^ ((r >> 3) & 1);  // inverse of swz128
+      const int chunk16 = swz128_chunk(r, slot & 7);
       const int oc = tile_n + r;
       base[j] = uint32_t(oc) * uint32_t(gemm_k) + uint32_t(chunk16 * 16);
       klim[j] = oc < gemm_n ? gemm_k - chunk16 * 16 : 0;
@@ -135,9 +135,9 @@ struct FilterRing {
 // zeros.  Copy q covers units [64j, 64j + 64) of row rr (q = rr *
 // row_copies + j), the four waves taking every fourth copy; copies never
 // straddle rows, so the row arithmetic is wave-uniform.  Unit `slot` of a
-// row is unit u of padded column pix (slot = pix*units + u); unit units-1
-// is the pad.  Its byte offset in x is
-//   ((b*h + iy)*w + pix - pad_w)*c + 16u = row_off + 16*(slot - pix).
+// row is unit u of padded column pix (slot = pix*units + u); units c/16 and
+// up are the pad.  Its byte offset in x is
+//   ((b*h + iy)*w + pix - pad_w)*c + 16u = row_off + pix*c + 16u.
 template <class Div>
 __device__ __forceinline__ void copy_input_rows(v4u xd, uint32_t lds0, int vr0, int nrows,
                                                 int wave, int lane, int row_copies,
@@ -157,9 +157,9 @@ __device__ __forceinline__ void copy_input_rows(v4u xd, uint32_t lds0, int vr0, 
     const uint32_t row_off = uint32_t((b * h + iy) * wd - pad_w) * uint32_t(c);
     const int slot = j * 64 + lane;
     const int pix = int(fast_div(uint32_t(slot), div_units));
-    const bool ok = row_ok && slot - pix * units < units - 1 &&
-                    unsigned(pix - pad_w) < unsigned(wd);
-    const uint32_t off = ok ? row_off + uint32_t(16 * (slot - pix)) : kOutOfRange;
+    const int u = slot - pix * units;
+    const bool ok = row_ok && u < (c >> 4) && unsigned(pix - pad_w) < unsigned(wd);
+    const uint32_t off = ok ? row_off + uint32_t(pix * c + 16 * u) : kOutOfRange;
     lds_copy16(xd, lds0 + rr * row_bytes + j * 1024, off);
   }
 }

@@ -313,24 +313,41 @@ __device__ __forceinline__ v4i mfma16(v4i a, v4i b, v4i c) {
 
 #endif  // __HIPCC__
 
+// LDS bank rule for ds_read_b128 on gfx950, measured with the LDS probe
+// (kernel_probe.hip): a wave's read runs at full rate when every 32
+// consecutive lanes address distinct 16-byte units modulo 512 bytes and
+// every 4 consecutive lanes distinct units modulo 128 bytes; a pattern that
+// breaks either takes about 1.4x as long (2-way), and 8 or 16 lanes on one
+// unit position 5.5x and 11x.  An MFMA fragment read has lane l on row
+// (or pixel) l % 16 and 16-byte chunk l / 16 (+ 4 for the second k-half),
+// so lanes 0..31 cover 16 rows x 2 chunks and lanes 4k..4k+3 four
+// consecutive rows of one chunk.
+
 // LDS layout of a [rows][128-byte] operand tile: 16-byte chunk j of row r
-// lives at r*128 + 16*(j ^ (r & 7) ^ ((r >> 3) & 1)).  Sixteen lanes reading
-// chunk j of rows r0..r0+15 (r0 % 16 == 0) hit sixteen distinct 16-byte
-// bank groups modulo 256 bytes, and any eight consecutive ones modulo 128.
-I8_HD inline int swz128(int row, int chunk) {
-  return row * 128 + ((chunk ^ (row & 7) ^ ((row >> 3) & 1)) << 4);
-}
+// lives at r*128 + 16*(j ^ f(r)) with f(r) = 2*((r + (r >> 2)) & 3) +
+// ((r >> 2) & 1).  Rows r, r + 4, r + 8, r + 12 share a 512-byte unit
+// position modulo 4 rows, and f gives them four distinct values of f >> 1,
+// so chunks j and j ^ 1 of the four land on eight distinct units; f of four
+// consecutive rows takes four distinct values.  (The earlier form
+// j ^ (r & 7) ^ ((r >> 3) & 1) broke the 32-lane condition: 123 against
+// 173 bytes per clock per compute unit in the probe.)
+I8_HD inline int swz128_f(int row) { return 2 * ((row + (row >> 2)) & 3) + ((row >> 2) & 1); }
+I8_HD inline int swz128(int row, int chunk) { return row * 128 + ((chunk ^ swz128_f(row)) << 4); }
+// Inverse: the logical chunk stored in physical 16-byte slot `phys` of
+// `row` (a DMA writes slots in order, so each lane fetches the chunk its
+// slot holds).
+I8_HD inline int swz128_chunk(int row, int phys) { return phys ^ swz128_f(row); }
 
 // LDS layout of a [pixels][64-byte] halo/strip patch: chunk j of pixel p at
-// p*64 + 16*(j ^ ((p >> 2) & 3)).  Sixteen consecutive pixels reading one
-// chunk (the 16 lanes of an MFMA fragment) cover all sixteen 16-byte bank
-// groups of gfx950's 64 x 4-byte LDS banks.
-I8_HD inline int swz64(int pixel, int chunk) {
-  return pixel * 64 + ((chunk ^ ((pixel >> 2) & 3)) << 4);
-}
-// Inverse: the logical chunk stored in physical 16-byte slot `phys` of
-// `pixel` (used when a DMA writes slots in order and each lane must fetch
-// the chunk its slot holds).
-I8_HD inline int swz64_chunk(int pixel, int phys) { return phys ^ ((pixel >> 2) & 3); }
+// p*64 + 16*(j ^ g(p)), g(p) = 2*(((p >> 1) ^ (p >> 3)) & 1).  Pixels p and
+// p + 8 share a unit position modulo 512 bytes and get g values 0 and 2, so
+// chunks j, j ^ 1 of both cover four distinct units; consecutive pixels p,
+// p + 2 of one parity get different g.  Conflict-free for sixteen
+// consecutive pixels by the rule above (the earlier j ^ ((p >> 2) & 3) was
+// not: 122 against 173 bytes per clock).
+I8_HD inline int swz64_g(int pixel) { return 2 * (((pixel >> 1) ^ (pixel >> 3)) & 1); }
+I8_HD inline int swz64(int pixel, int chunk) { return pixel * 64 + ((chunk ^ swz64_g(pixel)) << 4); }
+// Inverse, as for swz128_chunk.
+I8_HD inline int swz64_chunk(int pixel, int phys) { return phys ^ swz64_g(pixel); }
 
 }  // namespace i8conv

@@ -124,6 +124,11 @@ int rowpass_wait_expired(int *expired);
 // launch shape workgroups x threads with `lds` bytes of dynamic LDS.
 int launch_store_floor(int32_t *y, size_t bytes, int workgroups, int threads, size_t lds,
                        bool write_through, void *stream);
+// kernel_probe.hip: the LDS read probe, pattern 0..5 (linear, swz128,
+// stride128, stride256, xor_rows, pitch80), `iters` 16-byte reads per lane; sink holds
+// workgroups * threads int32.
+int launch_lds_probe(int pattern, int32_t *sink, int workgroups, int threads, int iters,
+                     void *stream);
 // Whether kernel_row.hip has an instance for 16*fn channels per wave, cg
 // 64-channel groups and nfr 16-column fragments per output row.
 bool row_instance_exists(int fn, int cg, int nfr);
@@ -146,9 +151,16 @@ inline size_t halo_ring_slot_bytes(int fn) { return size_t(64) * fn * 128; }
 struct HaloRowLayout {
   int64_t units, row_units, row_copies, row_bytes;
 };
-inline HaloRowLayout halo_row_layout(int64_t wp, int64_t c) {
+// Padding units after each pixel's c bytes: one for the halo kernel (an odd
+// pitch, whose strided fragment reads stay spread over the banks), two for
+// the row kernel (pitch c + 32: 2 x odd units for c % 64 == 0, which makes
+// its stride-1 fragment reads conflict-free by gfx950's ds_read_b128 bank
+// rule; with c + 16 they were 2-way conflicts).
+constexpr int kHaloPadUnits = 1;
+constexpr int kRowPadUnits = 2;
+inline HaloRowLayout halo_row_layout(int64_t wp, int64_t c, int pad_units) {
   HaloRowLayout l;
-  l.units = c / 16 + 1;
+  l.units = c / 16 + pad_units;
   l.row_units = wp * l.units;
   l.row_copies = (l.row_units + 63) / 64;
   const int64_t span = 64 * l.row_copies;

@@ -12,7 +12,7 @@
 //   * a ring of three stage buffers: stage s + 2 is in flight while stage s
 //     feeds the MFMAs, one barrier per stage; the copies of stage s + 2 are
 //     issued between the MFMA groups of stage s, or by copy waves (below);
-//   * the LDS rows use the conflict-free swz128 layout.  A copy writes lane
+//   * the LDS rows use the swz128 layout (conflict-free fragment reads).  A copy writes lane
 //     i's 16 bytes to LDS slot i of its 1 KB block, so the swizzle is applied
 //     on the source side: the lane of slot (row, physical chunk) fetches the
 //     logical chunk that belongs there;
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
 #pragma unroll
   for (int j = 0; j < CPA; ++j) {
     const int r = 8 * (wave + NW * j) + (lane >> 3);
-    const int lc = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1);  // inverse of swz128
+    const int lc = swz128_chunk(r, lane & 7);
     const int oc = tile_n + r;
     abase[j] = oc < a.gemm_n ? uint32_t(oc) * uint32_t(a.gemm_k) + uint32_t(lc * 16)
                              : kOutOfRange;
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
 #pragma unroll
   for (int j = 0; j < CPB; ++j) {
     const int r = 8 * (wave + NW * (CPA + j)) + (lane >> 3);  // >= BN
-    const int lc = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1);
+    const int lc = swz128_chunk(r, lane & 7);
     const int m = tile_m + r - BN;
     if (m < m_end) {
       const int b = int(fast_div(uint32_t(m), a.div_ohw));

@@ -280,7 +280,7 @@ bool halo_instance_exists(int fn, int steps) {
 }
 
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream) {
-  const HaloRowLayout row = halo_row_layout(a.wd + 2 * a.pad_w, a.c);
+  const HaloRowLayout row = halo_row_layout(a.wd + 2 * a.pad_w, a.c, kHaloPadUnits);
   const int fn = p.bn / 64;
   const size_t lds = size_t(kHaloBiasLds) + size_t(p.rows) * size_t(row.row_bytes) +
                      size_t(p.ring) * halo_ring_slot_bytes(fn);

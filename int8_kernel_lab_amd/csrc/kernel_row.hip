@@ -48,8 +48,8 @@ struct RowArgs {
   int out_h, out_w, gemm_n, gemm_k;
   int hp;           // padded rows per image: h + 2*pad_h
   int wp;           // padded columns: w + 2*pad_w (== out_w + 2)
-  int pitch;        // LDS bytes per input pixel: c + 16
-  int units;        // 16-byte units per pixel in LDS: c / 16 + 1
+  int pitch;        // LDS bytes per input pixel: c + 32
+  int units;        // 16-byte units per pixel in LDS: c / 16 + 2
   int row_copies;   // 1 KB copies per padded input row
   int row_bytes;    // LDS bytes between consecutive rows
   int input_bytes;  // LDS bytes of the input rows
@@ -322,7 +322,7 @@ int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream) {
   const int fn = p.bn / 64;
   const int cg = a.c / 64;
   const int nfr = (a.out_w + 15) / 16;
-  const HaloRowLayout row = halo_row_layout(a.wd + 2 * a.pad_w, a.c);
+  const HaloRowLayout row = halo_row_layout(a.wd + 2 * a.pad_w, a.c, kRowPadUnits);
   const size_t lds = size_t(kHaloBiasLds) + size_t(p.rows) * size_t(row.row_bytes) +
                      size_t(p.ring) * halo_ring_slot_bytes(fn);
   if (a.r != 3 || a.s != 3 || a.stride_h != 1 || a.stride_w != 1 || a.dil_h != 1 ||
@@ -351,7 +351,7 @@ int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream) {
   h.gemm_k = a.gemm_k;
   h.hp = a.h + 2 * a.pad_h;
   h.wp = a.wd + 2 * a.pad_w;
-  h.pitch = a.c + 16;
+  h.pitch = a.c + 16 * kRowPadUnits;
   h.units = int(row.units);
   h.row_copies = int(row.row_copies);
   h.row_bytes = int(row.row_bytes);

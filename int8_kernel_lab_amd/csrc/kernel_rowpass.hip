@@ -36,12 +36,15 @@
 // groups: the walk then runs twice, group 0 (accumulating every output row
 // of the block) and group 1 (completing and storing them).
 //
-// Layouts.  Input: one LDS plane per (group, padded row): wp pixels x 80
-// bytes (the group's 64 channels, then 16 bytes of padding), so the 16
-// pixels of a fragment hit 16 distinct 16-byte bank groups (pitch 5 units).
-// Filter: per MFMA wave, 18 1 KB halves (group-major, then tap): 16 output
-// channels x 64 bytes in the swz64 layout, copied with the swizzle applied
-// at the source.
+// Layouts.  Input: one LDS plane per (group, padded row): wp pixels x 96
+// bytes (the group's 64 channels, then 32 bytes of padding).  A fragment
+// read (16 pixels x 4 chunks) is then conflict-free by gfx950's
+// ds_read_b128 bank rule (i8conv_device.hpp): a pitch of 6 units puts
+// lanes 0..31 on 32 distinct units modulo 512 bytes and four consecutive
+// pixels on distinct units modulo 128; the earlier 80-byte pitch (5 units)
+// made every fragment read a 2-way conflict.  Filter: per MFMA wave, 18
+// 1 KB halves (group-major, then tap): 16 output channels x 64 bytes in the
+// swz64 layout, copied with the swizzle applied at the source.
 //
 // Reuse and MFMAs are as in kernel_row.hip: the fragment of input row ir at
 // column offset fx feeds output rows ir - fy for fy = 0, 1, 2.
@@ -61,7 +64,7 @@ __device__ __attribute__((aligned(4))) unsigned int g_wait_expired;
 namespace {
 
 constexpr int kGroups = 2;      // 64-channel groups: c == 128
-constexpr int kUnits = 5;       // 16-byte units per pixel in a plane (4 data + 1 pad)
+constexpr int kUnits = 6;       // 16-byte units per pixel in a plane (4 data + 2 pad)
 constexpr int kTaps = 9;
 constexpr int kHalves = kTaps * kGroups;  // 1 KB filter halves per wave
 // Channel groups per row walk: 2 (one pass over the rows, both groups per
@@ -85,7 +88,7 @@ struct PassArgs {
   int n, h, wd, c, pad_h, pad_w;
   int out_h, out_w, gemm_n, gemm_k;
   int hp, wp;        // padded rows per image, padded columns
-  int plane_copies;  // 1 KB copies per plane: ceil(wp * 5 / 64)
+  int plane_copies;  // 1 KB copies per plane: ceil(wp * kUnits / 64)
   int rows_in;       // input rows per block: R + 2
   int blocks, tiles_n;
   FastDiv3 div_plane_copies, div_hp, div_blocks, div_tiles_n;
@@ -515,8 +518,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     // Chunk (groups g0 .. g0 + ng - 1, row r): the bias (first chunk), the
     // filter taps of filter row r (r <= 2) and plane copies j = wave + 4i
     // of padded input row r.  Copy j covers units [64j, 64j + 64) of the
-    // plane; unit u of pixel pix is slot pix*5 + u (u == 4: padding, left
-    // out of range -> zeros).
+    // plane; unit u of pixel pix is slot pix*kUnits + u (u >= 4: padding,
+    // left out of range -> zeros).
     auto issue_chunk = [&](int g0, int r, int pw, int ng) {
       if (g0 == 0 && r == 0) stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, bias_lds, lane);
       for (int g = g0; g < g0 + ng; ++g) {
@@ -541,7 +544,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
           const int slot = j * 64 + lane;
           const int pix = slot / kUnits;
           const int u = slot - pix * kUnits;
-          const bool ok = row_ok && u < kUnits - 1 && unsigned(pix - p.pad_w) < unsigned(p.wd);
+          const bool ok = row_ok && u < 4 && unsigned(pix - p.pad_w) < unsigned(p.wd);
           const uint32_t off = ok ? row_off + uint32_t(64 * g + pix * p.c + 16 * u) : kOutOfRange;
           lds_copy16(xd, planes_lds + uint32_t((g * p.rows_in + r) * plane_bytes + j * 1024),
                      off);

@@ -196,7 +196,7 @@ bool plan_resident(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p
     const int64_t oy = (m % (int64_t(g.out_h) * g.out_w)) / g.out_w;
     return b * hp + oy * s.stride_h;
   };
-  const HaloRowLayout row = halo_row_layout(wp, s.c);
+  const HaloRowLayout row = halo_row_layout(wp, s.c, kHaloPadUnits);
   if (row.row_bytes > kLdsBudget) return false;
   const int64_t first = std::max<int64_t>(1, std::min(total_frags, ceil_div(256, tiles_n)));
   const int64_t chunks = ceil_div(g.gemm_k, 128);
@@ -247,7 +247,7 @@ bool plan_row(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
     return false;
   const int cg = s.c / 64;
   const int nfr = int(ceil_div(g.out_w, 16));
-  const HaloRowLayout row = halo_row_layout(int64_t(s.w) + 2 * s.pad_w, s.c);
+  const HaloRowLayout row = halo_row_layout(int64_t(s.w) + 2 * s.pad_w, s.c, kRowPadUnits);
   const int64_t chunks = ceil_div(g.gemm_k, 128);
   // For each channel slice width (16*fn channels per wave), the smallest
   // number of row blocks per image that gives every compute unit a

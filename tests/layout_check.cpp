@@ -1,0 +1,97 @@
+// Check of the LDS layouts the kernels read MFMA fragments from
+// (i8conv_device.hpp, i8conv_internal.hpp), built with g++ by
+// tests/test_host.py.  For every layout: the swizzle permutes the 16-byte
+// chunks of a row, its inverse undoes it, and every fragment read (lane l:
+// row or pixel l % 16 from a multiple of 16, chunk l / 16 of either
+// k-half) satisfies gfx950's ds_read_b128 bank rule as measured with the
+// LDS probe: 32 consecutive lanes on 32 distinct 16-byte units modulo 512
+// bytes and 4 consecutive lanes on 4 distinct units modulo 128 bytes.  The
+// same rule must reject the layouts the probe measured 2-way (an XOR of the
+// row's low bits, 80- and 144-byte pitches).  Prints "ok <checked>" or the
+// first failure; exit 0 on success.
+#include <stdio.h>
+
+#include <functional>
+#include <set>
+
+#include "i8conv_internal.hpp"
+
+using namespace i8conv;
+
+static int checked = 0;
+
+// unit(l): the 16-byte unit lane l reads
+static bool rule_ok(const std::function<long(int)> &unit) {
+  for (int h = 0; h < 64; h += 32) {
+    std::set<long> s;
+    for (int l = h; l < h + 32; ++l) s.insert(((unit(l) % 32) + 32) % 32);
+    if (s.size() != 32) return false;
+  }
+  for (int q = 0; q < 64; q += 4) {
+    std::set<long> s;
+    for (int l = q; l < q + 4; ++l) s.insert(((unit(l) % 8) + 8) % 8);
+    if (s.size() != 4) return false;
+  }
+  return true;
+}
+
+static bool expect(bool cond, const char *what, int a, int b) {
+  ++checked;
+  if (!cond) printf("FAIL %s (%d, %d)\n", what, a, b);
+  return cond;
+}
+
+int main() {
+  bool ok = true;
+  // swz128: 128-byte rows, 8 chunks
+  for (int r = 0; r < 512 && ok; ++r) {
+    std::set<int> phys;
+    for (int c = 0; c < 8; ++c) {
+      const int off = swz128(r, c);
+      ok &= expect(off / 128 == r, "swz128 stays in its row", r, c);
+      phys.insert((off % 128) / 16);
+      ok &= expect(swz128_chunk(r, (off % 128) / 16) == c, "swz128_chunk inverts swz128", r, c);
+    }
+    ok &= expect(phys.size() == 8, "swz128 permutes the chunks", r, 0);
+  }
+  for (int r0 = 0; r0 < 512 && ok; r0 += 16)
+    for (int kh = 0; kh < 2; ++kh)
+      ok &= expect(rule_ok([&](int l) { return swz128(r0 + l % 16, 4 * kh + l / 16) / 16; }),
+                   "swz128 fragment read conflict-free", r0, kh);
+  // swz64: 64-byte pixels, 4 chunks
+  for (int p = 0; p < 512 && ok; ++p) {
+    std::set<int> phys;
+    for (int c = 0; c < 4; ++c) {
+      const int off = swz64(p, c);
+      ok &= expect(off / 64 == p, "swz64 stays in its pixel", p, c);
+      phys.insert((off % 64) / 16);
+      ok &= expect(swz64_chunk(p, (off % 64) / 16) == c, "swz64_chunk inverts swz64", p, c);
+    }
+    ok &= expect(phys.size() == 4, "swz64 permutes the chunks", p, 0);
+  }
+  for (int p0 = 0; p0 < 512 && ok; p0 += 16)
+    ok &= expect(rule_ok([&](int l) { return swz64(p0 + l % 16, l / 16) / 16; }),
+                 "swz64 fragment read conflict-free", p0, 0);
+  // row kernel pitch: a fragment of 16 consecutive padded columns from any
+  // start, any 64-channel group and either k-half
+  for (int c = 64; c <= 1024 && ok; c += 64) {
+    const int units = int(halo_row_layout(64, c, kRowPadUnits).units);
+    for (int x0 = 0; x0 < 48 && ok; ++x0)
+      for (int ch = 0; ch < c / 16; ch += 4)
+        ok &= expect(rule_ok([&](int l) { return long(units) * (x0 + l % 16) + ch + l / 16; }),
+                     "row-kernel pitch conflict-free", c, x0);
+  }
+  // the rule rejects what the probe measured as 2-way
+  ok &= expect(!rule_ok([](int l) {
+                 const int r = l % 16;
+                 return long(r * 8 + ((l / 16) ^ (r & 7) ^ ((r >> 3) & 1)));
+               }),
+               "xor-of-row-bits layout rejected", 0, 0);
+  ok &= expect(!rule_ok([](int l) { return long(5 * (l % 16) + l / 16); }), "80-byte pitch rejected",
+               0, 0);
+  ok &= expect(!rule_ok([](int l) { return long(9 * (l % 16) + l / 16); }), "144-byte pitch rejected",
+               0, 0);
+  if (!ok) return 1;
+  printf("ok %d\n", checked);
+  return 0;
+}

@@ -7,6 +7,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 import int8_kernel_lab_amd as lab
@@ -254,6 +255,50 @@ def test_measure_graph_argument_errors_without_touching_the_gpu(baseline_cases):
     assert "poison_byte" in _lib.lib().i8conv_last_error().decode()
     bad = lab.ConvShape(1, 8, 8, 24, 8, 3, 3, 1, 1).c_struct()
     assert call(shape=bad) == _lib.BAD_SHAPE
+
+
+def test_lds_probe_argument_errors_without_touching_the_gpu():
+    # i8conv_measure_lds_probe checks pattern, shape, counts and the timing
+    # record before any HIP call
+    t = _lib.CGraphTiming()
+
+    def call(pattern=0, sink=FAKE, wg=256, threads=512, reads=17, iterations=5, timing=True):
+        return _lib.lib().i8conv_measure_lds_probe(
+            pattern, sink, wg, threads, reads, 0, 0.0, iterations, 5,
+            ctypes.byref(t) if timing else None)
+
+    assert call(pattern=6) == _lib.BAD_ARGUMENT
+    assert call(pattern=-1) == _lib.BAD_ARGUMENT
+    assert call(sink=None) == _lib.BAD_ARGUMENT
+    assert call(threads=100) == _lib.BAD_ARGUMENT
+    assert call(threads=2048) == _lib.BAD_ARGUMENT
+    assert call(wg=0) == _lib.BAD_ARGUMENT
+    assert call(reads=0) == _lib.BAD_ARGUMENT
+    assert call(iterations=0) == _lib.BAD_ARGUMENT
+    assert call(timing=False) == _lib.BAD_ARGUMENT
+    assert "pattern 0..5" in _lib.lib().i8conv_last_error().decode()
+
+
+def test_lds_probe_expected_values_follow_the_pattern():
+    # the host restatement of the probe's per-thread XOR: with one read per
+    # lane it is the fold of the one unit read, at the pattern's offset
+    def unit_fold(u):
+        return (u ^ (~u) ^ (3 * u) ^ (u ^ 0x55)) & 0xFFFFFFFF
+
+    lanes = np.arange(64)
+    offsets = {"linear": 16 * lanes, "stride128": 128 * lanes, "stride256": 256 * lanes,
+               "pitch80": 80 * (lanes % 16) + 16 * (lanes // 16)}
+    for pattern, off in offsets.items():
+        got = lab.lds_probe_expected(pattern, 64, 1).view(np.uint32).astype(np.int64)
+        assert (got == unit_fold(off // 16)).all(), pattern
+    # (swz128's offsets are the device layout function's; the GPU run checks
+    # the probe's stores against this restatement)
+    # two reads per lane at shifts 0 and 1: the folds of both units XORed
+    two = lab.lds_probe_expected("linear", 64, 2).view(np.uint32).astype(np.int64)
+    assert (two == (unit_fold(lanes) ^ unit_fold(lanes + 1024))).all()
+    # four reads per lane (each shift once), then eight (each shift twice: zero)
+    eight = lab.lds_probe_expected("stride256", 64, 8)
+    assert (eight == 0).all()
 
 
 def test_python_layer_raises_on_bad_calls(baseline_cases):

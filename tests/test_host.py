@@ -63,6 +63,18 @@ def test_fastdiv_is_exact(tmp_path):
     assert out.stdout.startswith("ok ")
 
 
+def test_lds_layouts_are_conflict_free(tmp_path):
+    # the fragment-read layouts (swz128, swz64, the row kernel's pixel pitch)
+    # permute chunks, invert, and satisfy the measured ds_read_b128 bank rule
+    exe = tmp_path / "layout_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-I", CSRC, "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "layout_check.cpp"), "-o", str(exe)],
+                   check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.startswith("ok ")
+
+
 # ---- workload tables (gen_case.py:15-36) ------------------------------------
 
 def test_workload_loader_errors(tmp_path):
