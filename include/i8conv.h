@@ -305,11 +305,12 @@ int i8conv_measure_store_floor(int32_t *output, size_t bytes, int workgroups,
 /* No counterpart in the reference: the control for the LDS bank-conflict
  * counters.  A kernel whose lanes only read LDS with ds_read_b128, 16 bytes
  * at a fixed per-lane pattern: 0 linear (lane l at 16*l: conflict-free), 1
- * the GEMM kernels' swz128 fragment read, 2 a 128-byte lane stride (two
- * 4-bank groups per 16 lanes), 3 a 256-byte stride (one group: the most
- * conflicting read there is), 4 an XOR swizzle of 128-byte rows and 5 an
- * 80-byte pixel pitch (both 2-way on gfx950 although each 16 lanes cover
- * all sixteen 4-bank groups); `iterations` reads per lane over 64 KB of
+ * a fragment read of the swz128 layout (the row kernels' filter ring), 2 a
+ * 128-byte lane stride (two 4-bank groups per 16 lanes), 3 a 256-byte
+ * stride (one group: the most conflicting read there is), 4 a fragment read
+ * of the swz128x layout (the pipelined GEMM's) and 5 an 80-byte pixel pitch
+ * (both 2-way on gfx950 although each 16 lanes cover all sixteen 4-bank
+ * groups); `iterations` reads per lane over 64 KB of
  * LDS, in `workgroups` x threads_per_workgroup (whole waves, at most 1024).
  * Timed as i8conv_measure_graph times a convolution, with `sink`
  * (workgroups * threads_per_workgroup int32, poison byte 0x5A) as its

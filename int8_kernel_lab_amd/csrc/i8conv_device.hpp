@@ -338,6 +338,18 @@ I8_HD inline int swz128(int row, int chunk) { return row * 128 + ((chunk ^ swz12
 // slot holds).
 I8_HD inline int swz128_chunk(int row, int phys) { return phys ^ swz128_f(row); }
 
+// The XOR-of-row-bits layout of 128-byte rows: chunk j of row r at
+// r*128 + 16*(j ^ (r & 7) ^ ((r >> 3) & 1)).  Each 16 lanes of a fragment
+// read cover all sixteen 4-bank groups, but it breaks the 32-lane
+// condition: fragment reads are 2-way conflicts.  The pipelined GEMM keeps
+// it all the same: there the conflict-free swz128 measured 1-2 % slower
+// (A/B, configs 3 and 5b and 256x256 layers; the GEMM's time is not in its
+// LDS reads), so swz128x is its layout.  Its own inverse.
+I8_HD inline int swz128x(int row, int chunk) {
+  return row * 128 + ((chunk ^ (row & 7) ^ ((row >> 3) & 1)) << 4);
+}
+I8_HD inline int swz128x_chunk(int row, int phys) { return phys ^ (row & 7) ^ ((row >> 3) & 1); }
+
 // LDS layout of a [pixels][64-byte] halo/strip patch: chunk j of pixel p at
 // p*64 + 16*(j ^ g(p)), g(p) = 2*(((p >> 1) ^ (p >> 3)) & 1).  Pixels p and
 // p + 8 share a unit position modulo 512 bytes and get g values 0 and 2, so

@@ -12,7 +12,7 @@
 //   * a ring of three stage buffers: stage s + 2 is in flight while stage s
 //     feeds the MFMAs, one barrier per stage; the copies of stage s + 2 are
 //     issued between the MFMA groups of stage s, or by copy waves (below);
-//   * the LDS rows use the swz128 layout (conflict-free fragment reads).  A copy writes lane
+//   * the LDS rows use the swz128x layout (see i8conv_device.hpp).  A copy writes lane
 //     i's 16 bytes to LDS slot i of its 1 KB block, so the swizzle is applied
 //     on the source side: the lane of slot (row, physical chunk) fetches the
 //     logical chunk that belongs there;
@@ -41,6 +41,7 @@ namespace i8conv {
 namespace {
 
 constexpr int kRing = 3;  // stage buffers in LDS
+constexpr int64_t kStreamOutputBytes = int64_t(128) << 20;
 
 typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
 
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
 #pragma unroll
   for (int j = 0; j < CPA; ++j) {
     const int r = 8 * (wave + NW * j) + (lane >> 3);
-    const int lc = swz128_chunk(r, lane & 7);
+    const int lc = swz128x_chunk(r, lane & 7);
     const int oc = tile_n + r;
     abase[j] = oc < a.gemm_n ? uint32_t(oc) * uint32_t(a.gemm_k) + uint32_t(lc * 16)
                              : kOutOfRange;
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
 #pragma unroll
   for (int j = 0; j < CPB; ++j) {
     const int r = 8 * (wave + NW * (CPA + j)) + (lane >> 3);  // >= BN
-    const int lc = swz128_chunk(r, lane & 7);
+    const int lc = swz128x_chunk(r, lane & 7);
     const int m = tile_m + r - BN;
     if (m < m_end) {
       const int b = int(fast_div(uint32_t(m), a.div_ohw));
@@ -212,10 +213,10 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
   for (int h = 0; h < 2; ++h) {
     const int ch = 4 * h + (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < FN; ++i) aoff[h][i] = swz128(wn * TNW + i * 16 + (lane & 15), ch);
+    for (int i = 0; i < FN; ++i) aoff[h][i] = swz128x(wn * TNW + i * 16 + (lane & 15), ch);
 #pragma unroll
     for (int j = 0; j < FM; ++j)
-      boff[h][j] = BN * kStageBytes + swz128(wm * TMW + j * 16 + (lane & 15), ch);
+      boff[h][j] = BN * kStageBytes + swz128x(wm * TMW + j * 16 + (lane & 15), ch);
   }
 
   v4i acc[FN][FM];
@@ -334,8 +335,36 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
       }
     }
   };
+  // Outputs beyond 128 MiB: fragment by fragment, evict-first.  Written
+  // through, such outputs ran up to 1.75x slower (16x256x256x256 1x1: 220
+  // -> 388 us; 268 MB and up all lost), while every output of the baseline
+  // layers (0.8-51 MB) gains from it.
+  auto store_tile_by_fragment = [&]() {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
+        if (px >= m_end) continue;
+        const v4i v = add_wrap(acc[i][j], bias[i]);
+        if (vec) {
+          if (oc0 < a.gemm_n)
+            store_out4<kStoreStream>(
+                ow.r, (uint32_t(px - tile_m) * uint32_t(a.gemm_n) + uint32_t(oc0)) * 4u, v);
+        } else {
+          int32_t *dst = out + size_t(px) * size_t(a.gemm_n) + oc0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (oc0 + e < a.gemm_n) store_out1(dst + e, v[e]);
+        }
+      }
+    }
+  };
   // one uniform branch for the whole epilogue
-  if (sector_pitch(a.gemm_n))
+  if (!kSplit && int64_t(a.gemm_m) * a.gemm_n * 4 > kStreamOutputBytes)
+    store_tile_by_fragment();
+  else if (sector_pitch(a.gemm_n))
     store_tile(std::integral_constant<int, kStoreThrough>{});
   else
     store_tile(std::integral_constant<int, 0>{});

@@ -15,13 +15,13 @@
 // SQ_LDS_IDX_ACTIVE).  The LDS has 64 banks of 4 bytes, so a 16-byte read
 // covers one of sixteen 4-bank groups modulo 256 bytes:
 //   0 linear    lane l at 16 * l: each 16 lanes cover all sixteen groups
-//   1 swz128    lane l at swz128(l % 16, l / 16): the fragment read of the
-//               GEMM kernels (sixteen distinct groups per 16 lanes)
+//   1 swz128    lane l at swz128(l % 16, l / 16): a fragment read of the
+//               row kernels' filter ring (conflict-free)
 //   2 stride128 lane l at 128 * l: two groups per 16 lanes (8-way)
 //   3 stride256 lane l at 256 * l: one group per 16 lanes (16-way)
-//   4 xor_rows  lane l at row l % 16 of 128-byte rows, chunk
-//               (l / 16) ^ (row & 7) ^ ((row >> 3) & 1): 16 distinct groups
-//               per 16 lanes, yet 2-way on gfx950 (its 32-lane condition)
+//   4 xor_rows  lane l at swz128x(l % 16, l / 16), the pipelined GEMM's
+//               layout: 16 distinct groups per 16 lanes, yet 2-way on
+//               gfx950 (its 32-lane condition)
 //   5 pitch80   lane l at 80 * (l % 16) + 16 * (l / 16): a 5-unit pixel
 //               pitch, 2-way on gfx950 likewise
 // Iteration i reads at pattern + 16384 * (i % 4) in 64 KB of LDS filled
@@ -95,8 +95,7 @@ __global__ __launch_bounds__(1024) void lds_probe_kernel(int32_t *sink, int iter
   else if constexpr (kPattern == 3)
     base = 256u * uint32_t(lane);
   else if constexpr (kPattern == 4) {
-    const int r = lane & 15;
-    base = uint32_t(r * 128 + (((lane >> 4) ^ (r & 7) ^ ((r >> 3) & 1)) << 4));
+    base = uint32_t(swz128x(lane & 15, lane >> 4));
   } else
     base = uint32_t(80 * (lane & 15) + 16 * (lane >> 4));
   v4i acc = v4i{0, 0, 0, 0};

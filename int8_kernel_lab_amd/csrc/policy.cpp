@@ -7,17 +7,23 @@
 //   1. the row-streaming 3x3 stride-1 kernel (a halo plan) whenever it has a
 //      plan: it won every layer it covers (ResNet/Darknet 3x3 stages,
 //      batched 56x56 and 28x28 layers, 14x14 C = 256);
-//   2. split-K when the generic grid cannot fill the chip (fewer than 128
-//      tiles) and the reduction is long (>= 16 stages of 128 k-bytes): deep
-//      7x7 / 13x13 / 14x14 layers and stride-2 downsamplers at batch 1;
+//   2. split-K when the generic grid is tiny (at most 16 tiles) and the
+//      reduction long: at least 16 stages of 128 k-bytes, or 8 for a 1x1
+//      filter (deep 7x7 / 13x13 / 14x14 layers and stride-2 downsamplers at
+//      batch 1: it won all of them; at 24 tiles and 18 stages the generic
+//      GEMM won, 15.0 vs 15.7 us, and on a 32x32 3x3 layer of 9 stages the
+//      halo kernel, 9.3 vs 11.0 us);
 //   3. the pipelined generic GEMM (C % 128 == 0) when its grid has at least
 //      128 tiles: large layers of any filter (it beat every halo/strip plan
 //      from 28x28 x 32 images up to 256x256 x 16, stride 1 or 2, 3x3 or 5x5,
 //      dilated or not);
-//   4. otherwise an input-reuse kernel for a spatial filter (r*s > 1): halo
-//      when eligible, else strip (small dilated layers, asymmetric 1x3/3x1,
-//      C = 64 layers wider than the row kernel's four fragments);
-//   5. otherwise the generic implicit GEMM (1x1 layers, C % 64 != 0).
+//   4. otherwise an input-reuse kernel for a stride-1 spatial filter
+//      (r*s > 1): halo when eligible, else strip (small dilated layers,
+//      asymmetric 1x3/3x1, C = 64 layers wider than the row kernel's four
+//      fragments); at stride 2 the generic GEMM beat the halo kernel on
+//      every such layer (15.0 vs 18.0 us at 52x52, C = 256);
+//   5. otherwise the generic implicit GEMM (1x1 layers, strided layers,
+//      C % 64 != 0).
 #include "i8conv_internal.hpp"
 
 namespace i8conv {
@@ -31,9 +37,11 @@ int dispatch(const i8conv_shape &s) {
   const GemmPlan gp = plan_generic(s, g);
   const int64_t tiles = ((g.gemm_m + gp.bm - 1) / gp.bm) *
                         ((int64_t(g.gemm_n) + gp.bn - 1) / gp.bn);
-  if (tiles < 128 && gp.stages >= 16) return I8CONV_KERNEL_SPLITK;
+  const bool spatial = int64_t(s.r) * s.s > 1;
+  if (tiles <= 16 && (gp.stages >= 16 || (!spatial && gp.stages >= 8)))
+    return I8CONV_KERNEL_SPLITK;
   if (gp.dma && tiles >= 128) return I8CONV_KERNEL_GENERIC;
-  if (int64_t(s.r) * s.s > 1) {
+  if (spatial && s.stride_h == 1 && s.stride_w == 1) {
     if (halo) return I8CONV_KERNEL_HALO;
     if (plan_strip(s, g, &pp)) return I8CONV_KERNEL_STRIP;
   }

@@ -58,6 +58,18 @@ int main() {
     for (int kh = 0; kh < 2; ++kh)
       ok &= expect(rule_ok([&](int l) { return swz128(r0 + l % 16, 4 * kh + l / 16) / 16; }),
                    "swz128 fragment read conflict-free", r0, kh);
+  // swz128x: a permutation of each row's chunks with its inverse (2-way by
+  // the rule: checked below)
+  for (int r = 0; r < 512 && ok; ++r) {
+    std::set<int> phys;
+    for (int c = 0; c < 8; ++c) {
+      const int off = swz128x(r, c);
+      ok &= expect(off / 128 == r, "swz128x stays in its row", r, c);
+      phys.insert((off % 128) / 16);
+      ok &= expect(swz128x_chunk(r, (off % 128) / 16) == c, "swz128x_chunk inverts swz128x", r, c);
+    }
+    ok &= expect(phys.size() == 8, "swz128x permutes the chunks", r, 0);
+  }
   // swz64: 64-byte pixels, 4 chunks
   for (int p = 0; p < 512 && ok; ++p) {
     std::set<int> phys;
@@ -82,11 +94,8 @@ int main() {
                      "row-kernel pitch conflict-free", c, x0);
   }
   // the rule rejects what the probe measured as 2-way
-  ok &= expect(!rule_ok([](int l) {
-                 const int r = l % 16;
-                 return long(r * 8 + ((l / 16) ^ (r & 7) ^ ((r >> 3) & 1)));
-               }),
-               "xor-of-row-bits layout rejected", 0, 0);
+  ok &= expect(!rule_ok([](int l) { return long(swz128x(l % 16, l / 16) / 16); }),
+               "swz128x (xor-of-row-bits) layout rejected", 0, 0);
   ok &= expect(!rule_ok([](int l) { return long(5 * (l % 16) + l / 16); }), "80-byte pitch rejected",
                0, 0);
   ok &= expect(!rule_ok([](int l) { return long(9 * (l % 16) + l / 16); }), "144-byte pitch rejected",
