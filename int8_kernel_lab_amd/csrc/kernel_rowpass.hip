@@ -228,6 +228,14 @@ struct PassState {
   template <int G, int IR>
   __device__ __forceinline__ void step(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                        int oc0, int lane) {
+    // Output row IR - 3, complete since the previous row's MFMAs, is stored
+    // first thing: its accumulators were last written a whole row of MFMAs
+    // ago (storing right after those MFMAs would stall the wave until they
+    // drained, every row), and its stores go out ahead of this row's MFMAs
+    // (5.67 -> 5.54 us per launch on 28x28x128 against storing at the end of
+    // the step).
+    if (G + NG == kGroups && IR >= OLO + 3)
+      store_row<(IR >= OLO + 3 ? IR - 3 : 0)>(p, vec, rows_out, m_row0, oc0, lane);
     v4i cur[NG][3][NFR];
 #pragma unroll
     for (int g = 0; g < NG; ++g)
@@ -267,12 +275,6 @@ struct PassState {
     // them, they held the MFMAs back: 6.7 -> 6.5 us per launch on 28x28x128)
     interleave<reads_in_step(IR), mfmas_in_step(IR)>(
         std::make_index_sequence<mfmas_in_step(IR)>{});
-    // Output row IR - 2 is complete after this row's MFMAs; it is stored one
-    // row later, so that its accumulators are read long after the MFMAs that
-    // wrote them (reading them right away would stall the wave until those
-    // MFMAs drained, every row).
-    if (G + NG == kGroups && IR >= OLO + 3)
-      store_row<(IR >= OLO + 3 ? IR - 3 : 0)>(p, vec, rows_out, m_row0, oc0, lane);
   }
 
   // Output row O: the accumulators already hold bias + dot products.  N % 4
