@@ -452,12 +452,21 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
     st.qshort = __builtin_amdgcn_ballot_w64(!ok) == 0;
   }
 
-  st.template walk<0>(p, vec, rows_out, m_row0, oc0, lane,
-                      std::make_index_sequence<OHI - OLO + 2>{});
-  if constexpr (NG == 1)
-    st.template walk<1>(p, vec, rows_out, m_row0, oc0, lane,
+  // The walk specialised for the (uniform) store path: each copy holds only
+  // its own stores, and the 16-byte path's row steps no longer jump over
+  // the element-store code (28x28x128: 5.52 -> 5.41 us per launch).
+  auto walks = [&](bool v) {
+    st.template walk<0>(p, v, rows_out, m_row0, oc0, lane,
                         std::make_index_sequence<OHI - OLO + 2>{});
-  st.template store_row<OHI - 1>(p, vec, rows_out, m_row0, oc0, lane);
+    if constexpr (NG == 1)
+      st.template walk<1>(p, v, rows_out, m_row0, oc0, lane,
+                          std::make_index_sequence<OHI - OLO + 2>{});
+    st.template store_row<OHI - 1>(p, v, rows_out, m_row0, oc0, lane);
+  };
+  if (vec)
+    walks(true);
+  else
+    walks(false);
 }
 
 // Output rows the MFMA waves walk when the copy waves take the rest of the
