@@ -51,6 +51,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <utility>
 
 #include "halo_common.hpp"
@@ -71,6 +72,10 @@ constexpr int kHalves = kTaps * kGroups;  // 1 KB filter halves per wave
 // row) where the registers allow it, 1 (two passes, group 0 then group 1)
 // for 4 fragments per row, whose single-pass form would spill.
 constexpr int walk_groups(int nfr) { return nfr == 4 ? 1 : 2; }
+// How a walk stores its output rows: element stores (a misaligned output or
+// N % 4 != 0); 16-byte stores, with a branch per row on the block's row
+// count; 16-byte stores of a block that has all the walk's rows (no branch).
+constexpr int kStoreElem = 0, kStoreVec = 1, kStoreFull = 2;
 
 // Everything the kernel reads; loaded into SGPRs in one batch.
 struct PassArgs {
@@ -177,15 +182,17 @@ struct PassState {
   // MFMAs and LDS reads (the next row's fragments and taps) of step ir.
   // Scheduling groups: MFMA m is preceded by the LDS reads that spread NR
   // reads evenly over NM MFMAs (ceil((m+1) NR / NM) - ceil(m NR / NM)).
-  template <int NR, int NM, int M>
+  // With NS > 0, the NS buffer stores of the step go right after MFMA SA.
+  template <int NR, int NM, int SA, int NS, int M>
   __device__ static __forceinline__ void interleave_one() {
     constexpr int r = ((M + 1) * NR + NM - 1) / NM - (M * NR + NM - 1) / NM;
     if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (NS > 0 && M == SA) __builtin_amdgcn_sched_group_barrier(0x040, NS, 0);
   }
-  template <int NR, int NM, size_t... M>
+  template <int NR, int NM, int SA, int NS, size_t... M>
   __device__ static __forceinline__ void interleave(std::index_sequence<M...>) {
-    (interleave_one<NR, NM, int(M)>(), ...);
+    (interleave_one<NR, NM, SA, NS, int(M)>(), ...);
   }
 
   template <int G>
@@ -225,17 +232,18 @@ struct PassState {
   // (compile-time valid ones); in the last walk, output row IR - 3 is then
   // stored.  The flags of the chunk after next are read here and tested
   // one row later, so a chunk that has landed costs no wait.
-  template <int G, int IR>
-  __device__ __forceinline__ void step(const PassArgs &p, bool vec, int rows_out, int m_row0,
-                                       int oc0, int lane) {
-    // Output row IR - 3, complete since the previous row's MFMAs, is stored
-    // first thing: its accumulators were last written a whole row of MFMAs
-    // ago (storing right after those MFMAs would stall the wave until they
-    // drained, every row), and its stores go out ahead of this row's MFMAs
-    // (5.67 -> 5.54 us per launch on 28x28x128 against storing at the end of
-    // the step).
-    if (G + NG == kGroups && IR >= OLO + 3)
-      store_row<(IR >= OLO + 3 ? IR - 3 : 0)>(p, vec, rows_out, m_row0, oc0, lane);
+  template <int G, int IR, int kMode>
+  __device__ __forceinline__ void step(const PassArgs &p, int rows_out, int m_row0, int oc0,
+                                       int lane) {
+    // Output row IR - 3 was completed by the previous row's MFMAs.
+    // kStoreFull: its two stores go between this row's MFMAs, after the
+    // sixth, by which time the MFMAs that completed it have drained.
+    // Otherwise (a branch per row: element stores, or a block with fewer
+    // rows than the walk) it is stored first thing.
+    constexpr bool kStoreHere = G + NG == kGroups && IR >= OLO + 3;
+    constexpr bool kInStep = kStoreHere && !kQ && kMode == kStoreFull;
+    if constexpr (kStoreHere && !kInStep)
+      store_row<IR - 3>(p, kMode != kStoreElem, rows_out, m_row0, oc0, lane);
     v4i cur[NG][3][NFR];
 #pragma unroll
     for (int g = 0; g < NG; ++g)
@@ -271,10 +279,17 @@ struct PassState {
         }
       }
     }
+    if constexpr (kInStep) {
+#pragma unroll
+      for (int j = 0; j < NFR; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(acc[IR - 3][j], yr, voff[j],
+                                               (IR - 3) * row_stride, kStoreThrough);
+    }
     // the next row's reads go between this row's MFMAs (issued all ahead of
     // them, they held the MFMAs back: 6.7 -> 6.5 us per launch on 28x28x128)
-    interleave<reads_in_step(IR), mfmas_in_step(IR)>(
-        std::make_index_sequence<mfmas_in_step(IR)>{});
+    constexpr int kNM = mfmas_in_step(IR);
+    interleave<reads_in_step(IR), kNM, (kNM < 6 ? kNM - 1 : 5), (kInStep ? NFR : 0)>(
+        std::make_index_sequence<kNM>{});
   }
 
   // Output row O: the accumulators already hold bias + dot products.  N % 4
@@ -337,9 +352,9 @@ struct PassState {
   }
 
   // The walk from group G over padded input rows OLO .. OHI + 1.
-  template <int G, size_t... I>
-  __device__ __forceinline__ void walk(const PassArgs &p, bool vec, int rows_out, int m_row0,
-                                       int oc0, int lane, std::index_sequence<I...>) {
+  template <int G, int kMode, size_t... I>
+  __device__ __forceinline__ void walk(const PassArgs &p, int rows_out, int m_row0, int oc0,
+                                       int lane, std::index_sequence<I...>) {
     flag_wait(counter<G>(p, OLO));
     peeked = flag_peek(counter<G>(p, OLO + 1));
     take_taps<G, 0>(lane);
@@ -352,7 +367,7 @@ struct PassState {
 #pragma unroll
         for (int j = 0; j < NFR; ++j) acc[r][j] = bv;
     }
-    (step<G, OLO + int(I)>(p, vec, rows_out, m_row0, oc0, lane), ...);
+    (step<G, OLO + int(I), kMode>(p, rows_out, m_row0, oc0, lane), ...);
   }
 };
 
@@ -455,18 +470,21 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
   // The walk specialised for the (uniform) store path: each copy holds only
   // its own stores, and the 16-byte path's row steps no longer jump over
   // the element-store code (28x28x128: 5.52 -> 5.41 us per launch).
-  auto walks = [&](bool v) {
-    st.template walk<0>(p, v, rows_out, m_row0, oc0, lane,
-                        std::make_index_sequence<OHI - OLO + 2>{});
+  auto walks = [&](auto mode) {
+    constexpr int M = decltype(mode)::value;
+    st.template walk<0, M>(p, rows_out, m_row0, oc0, lane,
+                           std::make_index_sequence<OHI - OLO + 2>{});
     if constexpr (NG == 1)
-      st.template walk<1>(p, v, rows_out, m_row0, oc0, lane,
-                          std::make_index_sequence<OHI - OLO + 2>{});
-    st.template store_row<OHI - 1>(p, v, rows_out, m_row0, oc0, lane);
+      st.template walk<1, M>(p, rows_out, m_row0, oc0, lane,
+                             std::make_index_sequence<OHI - OLO + 2>{});
+    st.template store_row<OHI - 1>(p, M != kStoreElem, rows_out, m_row0, oc0, lane);
   };
-  if (vec)
-    walks(true);
+  if (vec && !kQ && rows_out >= OHI)
+    walks(std::integral_constant<int, kStoreFull>{});
+  else if (vec)
+    walks(std::integral_constant<int, kStoreVec>{});
   else
-    walks(false);
+    walks(std::integral_constant<int, kStoreElem>{});
 }
 
 // Output rows the MFMA waves walk when the copy waves take the rest of the
