@@ -79,6 +79,12 @@ EDGE = {
     "stream_split_r4_nfr1": lab.ConvShape(32, 16, 16, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r5_w29": lab.ConvShape(32, 19, 29, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r6_k96": lab.ConvShape(32, 22, 13, 128, 96, 3, 3, 1, 1, 1, 1, 1, 1),
+    # deep channels, few pixels (the split-K regime): 32 slices of 128
+    # channels with an output-channel tail of 4 and no padding; padding 2;
+    # 14x14 images.
+    "deepc_k260_pad0": lab.ConvShape(4, 5, 9, 4096, 260, 3, 3, 0, 0, 1, 1, 1, 1),
+    "deepc_pad2": lab.ConvShape(2, 6, 6, 2048, 512, 3, 3, 2, 2, 1, 1, 1, 1),
+    "deepc_14x14": lab.ConvShape(2, 14, 14, 1024, 512, 3, 3, 1, 1, 1, 1, 1, 1),
 }
 
 _expected_cache = {}
