@@ -79,6 +79,12 @@ EDGE = {
     "stream_split_r4_nfr1": lab.ConvShape(32, 16, 16, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r5_w29": lab.ConvShape(32, 19, 29, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r6_k96": lab.ConvShape(32, 22, 13, 128, 96, 3, 3, 1, 1, 1, 1, 1, 1),
+    # c == 128 3x3 stride 2 (config 3's family): a 4-channel tail in the
+    # second 128-channel tile; no padding with odd input sizes and 64
+    # channels; 20-column output rows with a 72-channel tail.
+    "s2_k132": lab.ConvShape(64, 28, 28, 128, 132, 3, 3, 1, 1, 2, 2, 1, 1),
+    "s2_pad0_odd_k64": lab.ConvShape(32, 27, 27, 128, 64, 3, 3, 0, 0, 2, 2, 1, 1),
+    "s2_w40_k200": lab.ConvShape(16, 40, 40, 128, 200, 3, 3, 1, 1, 2, 2, 1, 1),
     # deep channels, few pixels (the split-K regime): 32 slices of 128
     # channels with an output-channel tail of 4 and no padding; padding 2;
     # 14x14 images.
