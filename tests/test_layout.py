@@ -76,9 +76,17 @@ def _run_gpu(fn, src: np.ndarray, out_elems: int, out_dtype, *args):
     return out
 
 
-TRANSPOSE_CASES = [  # (n, c, h, w): tiled (16-byte rows) and element forms, partial tiles
-    (2, 128, 28, 28), (1, 64, 16, 16), (3, 48, 5, 5), (2, 16, 33, 17), (1, 256, 7, 7),
-    (2, 130, 9, 7),
+TRANSPOSE_CASES = [  # (n, c, h, w)
+    # tiled (16-byte rows both ways): one or two 128-column tiles per
+    # workgroup, partial tiles
+    (2, 128, 28, 28), (1, 64, 16, 16), (1, 512, 16, 16),
+    # one side short (H x W or C not a multiple of 16): the short-row /
+    # short-column forms, with 128, 112 and 16 rows (or columns) per
+    # workgroup and a partial last one
+    (3, 48, 5, 5), (2, 16, 33, 17), (1, 256, 7, 7), (2, 1024, 7, 7), (1, 400, 14, 14),
+    (2, 64, 17, 17), (1, 32, 45, 45),
+    # element form: neither side fits
+    (2, 130, 9, 7), (1, 16, 47, 47),
 ]
 
 
@@ -98,7 +106,9 @@ def test_nchw_nhwc_round_trip_bit_exact(n, c, h, w):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n,h,w,k", [(2, 28, 28, 128), (3, 7, 7, 36), (1, 9, 11, 63), (2, 33, 3, 256)])
+@pytest.mark.parametrize("n,h,w,k", [  # tiled, short columns (H x W rows), short rows, elements
+    (2, 28, 28, 128), (2, 4, 4, 52), (3, 7, 7, 36), (2, 33, 3, 256), (2, 7, 7, 520),
+    (1, 14, 14, 2048), (1, 2, 2, 37), (2, 6, 6, 99), (1, 9, 11, 63)])
 def test_nhwk_to_nkhw_int32_bit_exact(n, h, w, k):
     from tests.conftest import say
     rng = np.random.default_rng(k)
