@@ -293,6 +293,12 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
   auto tiles = [](int64_t a, int64_t b) { return std::to_string((a + b - 1) / b); };
   if (id == I8CONV_KERNEL_GENERIC || id == I8CONV_KERNEL_SPLITK) {
     const GemmPlan p = id == I8CONV_KERNEL_GENERIC ? plan_generic(*shape, g) : plan_splitk(*shape, g);
+    if (p.deep)
+      d = std::string(kNames[id]) + " deep-channel: all " + std::to_string(g.gemm_m) +
+          "px x 32oc per workgroup, grid " + std::to_string(p.deep_plan.tiles_n) + "x" +
+          std::to_string(p.splits) + " splits of 128 channels, " +
+          std::to_string(p.deep_plan.lds / 1024) + " KB LDS, ordered reduce";
+    else
     d = std::string(kNames[id]) + (p.dma ? " pipelined" : " register-staged") + " tile " +
         std::to_string(p.bm) + "px x " + std::to_string(p.bn) + "oc" +
         (p.m_step > 0 && p.m_step < p.bm ? " (" + std::to_string(p.m_step) + "px stored)" : "") +
@@ -686,7 +692,12 @@ int i8conv_wait_expired(int *expired) {
     set_error("wait_expired needs an output");
     return I8CONV_BAD_ARGUMENT;
   }
-  return rowpass_wait_expired(expired);
+  int row = 0, deep = 0;
+  int rc = rowpass_wait_expired(&row);
+  if (rc == I8CONV_OK) rc = deepk_wait_expired(&deep);
+  if (rc != I8CONV_OK) return rc;
+  *expired = row | deep;
+  return I8CONV_OK;
 }
 
 int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,

@@ -23,6 +23,21 @@ int derive(const i8conv_shape &s, i8conv_geometry *g);
 // ---- generic / split-K -----------------------------------------------------
 // Workgroup tile of the staged implicit GEMM: BM output pixels x BN output
 // channels, k staged 128 bytes at a time.
+// Deep-channel split-K plan (kernel_deepk.hip): a workgroup per (128-channel
+// input slice, 32-channel output tile) over all M pixels; planes and filter
+// layout in LDS (16-byte units).
+constexpr int kDeepMaxFrags = 8;  // 16-pixel fragments per MFMA wave (M <= 512)
+constexpr int kDeepMaxLoadsPerWave = 24;  // 1 KB plane loads per copy wave (<= 768 pixels)
+struct DeepPlan {
+  int S = 0, I = 0;       // plane row / image strides
+  int loads = 0;          // 1 KB plane loads (8 input pixels each)
+  int frags = 0, nf = 0;  // fragments over M, per MFMA wave
+  int splits = 0, tiles_n = 0;
+  int flags_lds = 0, planes_lds = 0;
+  size_t lds = 0;
+};
+bool plan_deepk(const i8conv_shape &s, const i8conv_geometry &g, DeepPlan *out);
+
 struct GemmPlan {
   int bm = 0, bn = 0;
   int splits = 1;            // > 1 only for split-K
@@ -34,6 +49,9 @@ struct GemmPlan {
   // c % 128 == 0: the LDS-DMA pipelined kernel (kernel_gemm_dma.hip), else
   // the register-staged one (kernel_gemm.hip)
   bool dma = false;
+  // split-K only: the deep-channel kernel instead of the GEMM
+  bool deep = false;
+  DeepPlan deep_plan;
 };
 bool gemm_tile_supported(int bm, int bn);
 bool gemm_dma_tile_supported(int bm, int bn);
@@ -119,6 +137,8 @@ size_t rowpass_lds_bytes(int wp, int rows);
 // kernel_rowpass.hip: reads and clears the device word its waves set when a
 // bounded wait gives up (synchronizes the device); *expired = 1 if it was set.
 int rowpass_wait_expired(int *expired);
+int launch_deepk(const ConvArgs &a, const DeepPlan &p, void *workspace, void *stream);
+int deepk_wait_expired(int *expired);
 // kernel_probe.hip: a store-only kernel (16-byte buffer stores, write-through
 // or ordinary) over `bytes` of y (a multiple of 16, below 2^31) in the
 // launch shape workgroups x threads with `lds` bytes of dynamic LDS.

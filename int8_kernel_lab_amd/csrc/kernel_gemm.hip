@@ -320,7 +320,9 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
   args.partial = static_cast<int32_t *>(workspace);
   args.splits = p.splits;
   args.stages_per_split = p.stages_per_split;
-  int rc = p.dma ? launch_gemm_dma(args, p, p.splits, stream) : launch_any(args, p, p.splits, s);
+  int rc = p.deep  ? launch_deepk(args, p.deep_plan, workspace, stream)
+           : p.dma ? launch_gemm_dma(args, p, p.splits, stream)
+                   : launch_any(args, p, p.splits, s);
   if (rc != I8CONV_OK) return rc;
   const size_t total = size_t(a.gemm_m) * size_t(a.gemm_n);
   const bool vec = (a.gemm_n & 3) == 0 &&

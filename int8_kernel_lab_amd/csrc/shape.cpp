@@ -146,6 +146,17 @@ GemmPlan plan_generic(const i8conv_shape &s, const i8conv_geometry &g) {
 GemmPlan plan_splitk(const i8conv_shape &s, const i8conv_geometry &g) {
   GemmPlan p;
   p.stages = int(ceil_div(g.gemm_k, kStageBytes));
+  // 3x3 stride-1 layers whose output pixels all fit one workgroup's LDS
+  // planes: the deep-channel kernel, one split per 128 input channels
+  if (plan_deepk(s, g, &p.deep_plan)) {
+    p.deep = true;
+    p.dma = true;
+    p.bm = int(g.gemm_m);
+    p.bn = 32;
+    p.splits = p.deep_plan.splits;
+    p.stages_per_split = int(ceil_div(9 * 128, kStageBytes));
+    return p;
+  }
   p.dma = dma_eligible(s);
   if (p.dma) {
     p.bn = g.gemm_n <= 64 ? 64 : 128;

@@ -185,6 +185,26 @@ def test_dispatch_returns_an_eligible_kernel_with_its_workspace(name, shape):
     assert lab.describe(chosen, shape).startswith(chosen)
 
 
+def test_splitk_deep_channel_form_and_its_workspace(baseline_cases):
+    # 3x3 stride-1 layers with c % 128 == 0, c >= 256 and at most 512 output
+    # pixels take split-K's deep-channel form: one split per 128 input
+    # channels, 32-channel tiles over all pixels
+    cfg5a = baseline_cases["cfg5a_deep_k"]
+    d = lab.describe("splitk", cfg5a)
+    assert "deep-channel" in d and "grid 16x16 splits" in d, d
+    g = cfg5a.geometry()
+    assert lab.workspace_bytes("splitk", cfg5a) == (2048 // 128) * 4 * g.output_elements
+    deep = lab.ConvShape(2, 16, 16, 256, 64, 3, 3, 1, 1, 1, 1, 1, 1)     # M = 512
+    assert "deep-channel" in lab.describe("splitk", deep)
+    assert lab.workspace_bytes("splitk", deep) == 2 * 4 * deep.geometry().output_elements
+    for other in [lab.ConvShape(3, 16, 11, 256, 64, 3, 3, 1, 1, 1, 1, 1, 1),   # M = 528
+                  lab.ConvShape(8, 7, 7, 128, 64, 3, 3, 1, 1, 1, 1, 1, 1),    # c = 128
+                  lab.ConvShape(8, 7, 7, 320, 64, 3, 3, 1, 1, 1, 1, 1, 1),    # c % 128
+                  lab.ConvShape(8, 14, 14, 256, 64, 3, 3, 1, 1, 2, 2, 1, 1),  # stride 2
+                  lab.ConvShape(8, 7, 7, 256, 66, 3, 3, 1, 1, 1, 1, 1, 1)]:   # N % 4
+        assert "deep-channel" not in lab.describe("splitk", other), other
+
+
 def test_describe_errors_and_truncation(baseline_cases):
     shape = baseline_cases["cfg3_down_3x3_s2"]
     buf = ctypes.create_string_buffer(8)

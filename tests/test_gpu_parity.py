@@ -91,6 +91,15 @@ EDGE = {
     "deepc_k260_pad0": lab.ConvShape(4, 5, 9, 4096, 260, 3, 3, 0, 0, 1, 1, 1, 1),
     "deepc_pad2": lab.ConvShape(2, 6, 6, 2048, 512, 3, 3, 2, 2, 1, 1, 1, 1),
     "deepc_14x14": lab.ConvShape(2, 14, 14, 1024, 512, 3, 3, 1, 1, 1, 1, 1, 1),
+    # split-K's deep-channel form (every output pixel in one workgroup): 40
+    # one-pixel images (halo only, 41 chunk flags); 3 slices with a 36-channel
+    # tail; no padding with a 13-pixel last fragment; one-column images; 512
+    # pixels (eight fragments per MFMA wave, the largest plan)
+    "deepk_many_images_1x1": lab.ConvShape(40, 1, 1, 256, 32, 3, 3, 1, 1, 1, 1, 1, 1),
+    "deepk_k36_c384": lab.ConvShape(2, 7, 7, 384, 36, 3, 3, 1, 1, 1, 1, 1, 1),
+    "deepk_pad0_m_tail": lab.ConvShape(3, 9, 11, 256, 64, 3, 3, 0, 0, 1, 1, 1, 1),
+    "deepk_w1_rows": lab.ConvShape(4, 12, 1, 256, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    "deepk_m512": lab.ConvShape(2, 16, 16, 256, 64, 3, 3, 1, 1, 1, 1, 1, 1),
 }
 
 _expected_cache = {}
