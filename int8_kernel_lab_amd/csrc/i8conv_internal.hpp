@@ -27,6 +27,22 @@ int derive(const i8conv_shape &s, i8conv_geometry *g);
 // input slice, 32-channel output tile) over all M pixels; planes and filter
 // layout in LDS (16-byte units).
 constexpr int kDeepMaxFrags = 8;  // 16-pixel fragments per MFMA wave (M <= 512)
+// Planes: padded input pixel (b, row, col) at 16-byte unit b*I + row*S +
+// col*kDeepUnits (8 data units, 2 zero).  S = 10 out_w and I = 10 out_h out_w
+// modulo 32 units keep 16 consecutive output pixels 10 units apart modulo
+// 512 bytes across row and image boundaries (conflict-free B fragment
+// reads; tests/layout_check.cpp).
+constexpr int kDeepUnits = 10;
+inline int64_t deep_up_mod32(int64_t v, int64_t target) {
+  const int64_t t = ((target % 32) + 32) % 32;
+  return v + ((t - v % 32) + 32) % 32;
+}
+inline int64_t deep_row_units(int64_t wp, int64_t out_w) {
+  return deep_up_mod32(wp * kDeepUnits, 10 * out_w);
+}
+inline int64_t deep_image_units(int64_t hp, int64_t row_units, int64_t out_h, int64_t out_w) {
+  return deep_up_mod32(hp * row_units, 10 * out_h * out_w);
+}
 constexpr int kDeepMaxLoadsPerWave = 24;  // 1 KB plane loads per copy wave (<= 768 pixels)
 struct DeepPlan {
   int S = 0, I = 0;       // plane row / image strides

@@ -61,7 +61,7 @@ __device__ __attribute__((aligned(4))) unsigned int g_deepk_wait_expired;
 
 namespace {
 
-constexpr int kDkUnits = 10;                  // 16-byte units per plane pixel
+constexpr int kDkUnits = kDeepUnits;          // 16-byte units per plane pixel
 constexpr int kDkFilterBytes = 9 * 2 * 2048;  // taps x fragments x 16 rows x 128 B
 constexpr int kDkSpinLimit = 1 << 20;         // polls of about 64 cycles each
 constexpr int kDkMaxLoads = kDeepMaxLoadsPerWave;  // plane loads per copy wave
@@ -357,13 +357,8 @@ bool plan_deepk(const i8conv_shape &s, const i8conv_geometry &g, DeepPlan *out) 
   const int64_t frags = (g.gemm_m + 15) / 16;
   const int64_t nf = (frags + 3) / 4;
   if (nf > kDeepMaxFrags) return false;
-  auto up_mod32 = [](int64_t v, int64_t target) {
-    const int64_t t = ((target % 32) + 32) % 32;
-    while (v % 32 != t) ++v;
-    return v;
-  };
-  const int64_t S = up_mod32(wp * kDkUnits, 10 * int64_t(g.out_w));
-  const int64_t I = up_mod32(hp * S, 10 * int64_t(g.out_h) * g.out_w);
+  const int64_t S = deep_row_units(wp, g.out_w);
+  const int64_t I = deep_image_units(hp, S, g.out_h, g.out_w);
   const int64_t units = int64_t(s.n) * I;
   const int64_t loads = (int64_t(s.n) * s.h * s.w + 7) / 8;
   if ((loads + 3) / 4 > kDkMaxLoads) return false;

@@ -93,6 +93,35 @@ int main() {
         ok &= expect(rule_ok([&](int l) { return long(units) * (x0 + l % 16) + ch + l / 16; }),
                      "row-kernel pitch conflict-free", c, x0);
   }
+  // deep-channel split-K planes: every full 16-pixel fragment of every
+  // shape (images n, output h x w; the padded image is the output plus 2
+  // for a 3x3 stride-1 filter whatever the padding), at every tap and
+  // k-half, with the row and image strides of deep_row_units /
+  // deep_image_units
+  for (int oh = 1; oh <= 20 && ok; ++oh)
+    for (int ow = 1; ow <= 20 && ok; ++ow)
+      for (int n = 1; n <= 8 && ok; ++n) {
+          const long M = long(n) * oh * ow;
+          if (M > 512) break;
+          const long hp = oh + 2, wp = ow + 2;  // 3x3, stride 1: out = padded - 2
+          const long S = deep_row_units(wp, ow), I = deep_image_units(hp, S, oh, ow);
+          for (long f = 0; (f + 1) * 16 <= M && ok; ++f)
+            for (int t = 0; t < 9 && ok; ++t)
+              for (int kh = 0; kh < 2; ++kh)
+                ok &= expect(rule_ok([&](int l) {
+                               const long m = 16 * f + l % 16;
+                               const long b = m / (oh * ow), rem = m % (oh * ow);
+                               return b * I + (rem / ow) * S + (rem % ow) * kDeepUnits +
+                                      (t / 3) * S + (t % 3) * kDeepUnits + 4 * kh + l / 16;
+                             }),
+                             "deep-channel plane fragment conflict-free", int(M), int(f));
+      }
+  // without the row alignment (S = 10 wp) the 7x7 fragments conflict
+  ok &= expect(!rule_ok([](int l) {
+                 const long m = l % 16, S = 90;
+                 return (m / 7) * S + (m % 7) * kDeepUnits + l / 16;
+               }),
+               "unaligned deep-channel rows rejected", 0, 0);
   // the rule rejects what the probe measured as 2-way
   ok &= expect(!rule_ok([](int l) { return long(swz128x(l % 16, l / 16) / 16); }),
                "swz128x (xor-of-row-bits) layout rejected", 0, 0);
