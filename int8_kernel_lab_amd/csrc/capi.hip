@@ -299,7 +299,12 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
           std::to_string(p.splits) + " splits of 128 channels, " +
           std::to_string(p.deep_plan.lds / 1024) + " KB LDS, ordered reduce";
     else
-    d = std::string(kNames[id]) + (p.dma ? " pipelined" : " register-staged") + " tile " +
+    d = std::string(kNames[id]) +
+        (p.pw ? " pointwise streaming: filter in registers, 16px fragments x " +
+                    std::to_string(g.gemm_n) + "oc, " + std::to_string(p.pw_waves) +
+                    " waves; unaligned pointers:"
+              : "") +
+        (p.dma ? " pipelined" : " register-staged") + " tile " +
         std::to_string(p.bm) + "px x " + std::to_string(p.bn) + "oc" +
         (p.m_step > 0 && p.m_step < p.bm ? " (" + std::to_string(p.m_step) + "px stored)" : "") +
         ", grid " + tiles(g.gemm_m, p.m_step > 0 ? p.m_step : p.bm) + "x" +

@@ -246,6 +246,8 @@ __device__ __forceinline__ v4i load_bias4(const int32_t *base, int count, int i0
 // such layers several times slower).
 constexpr int kStoreThrough = 16;
 constexpr int kStoreStream = 2;
+// Final outputs above this size store evict-first instead of write-through.
+constexpr int64_t kStreamOutputBytes = int64_t(128) << 20;
 
 template <int kPolicy>
 __device__ __forceinline__ void store_out4(__amdgpu_buffer_rsrc_t out, uint32_t byte_off, v4i v) {

@@ -68,6 +68,12 @@ struct GemmPlan {
   // split-K only: the deep-channel kernel instead of the GEMM
   bool deep = false;
   DeepPlan deep_plan;
+  // generic only: 1x1 stride-1 unpadded layer whose filter fits a wave's
+  // registers, run by the pointwise streaming kernel (kernel_pointwise.hip)
+  // when the four pointers are 16-byte aligned; the tile fields above then
+  // describe the fallback GEMM for unaligned pointers
+  bool pw = false;
+  int pw_waves = 0;
 };
 bool gemm_tile_supported(int bm, int bn);
 bool gemm_dma_tile_supported(int bm, int bn);
@@ -121,6 +127,15 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
                   void *stream);
 // kernel_gemm_dma.hip; splits > 1 writes partial sums to a.partial
 int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stream);
+// kernel_pointwise.hip: C and N with an instance (N / 16 even, C % 64 == 0,
+// N * C <= 16384, C and N powers of two times 64 and 32), its launch, and
+// the pointer alignment it needs (16 bytes each)
+constexpr int kPwWaves = 2;        // waves per workgroup
+constexpr int kPwMaxWaves = 1024;  // waves per launch, at most
+bool pointwise_supported(int c, int n);
+int pointwise_waves(int64_t gemm_m);
+int launch_pointwise(const ConvArgs &a, void *stream);
+bool pointwise_pointers_ok(const ConvArgs &a);
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream);

@@ -41,7 +41,6 @@ namespace i8conv {
 namespace {
 
 constexpr int kRing = 3;  // stage buffers in LDS
-constexpr int64_t kStreamOutputBytes = int64_t(128) << 20;
 
 typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
 

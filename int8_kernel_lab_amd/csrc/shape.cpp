@@ -112,11 +112,37 @@ int gemm_dma_step(int64_t gemm_m, int64_t tiles_n, int bm, int bn) {
   return best;
 }
 
+// Pointwise streaming form: instances for N / 16 in {2, 4, 8, 16} and
+// C / 64 in {1, 2, 4, 8} with N * C <= 16384 (the filter as MFMA A operands
+// takes N * C / 1024 VGPRs per lane: at most 64).
+bool pointwise_supported(int c, int n) {
+  const bool cs = c == 64 || c == 128 || c == 256 || c == 512;
+  const bool ns = n == 32 || n == 64 || n == 128 || n == 256;
+  return cs && ns && int64_t(c) * n <= 16384;
+}
+
+int pointwise_waves(int64_t gemm_m) {
+  const int64_t nfrag = ceil_div(gemm_m, 16);
+  return int(std::min<int64_t>(nfrag, kPwMaxWaves));
+}
+
+static bool pointwise_eligible(const i8conv_shape &s, const i8conv_geometry &g) {
+  // 32-bit buffer offsets: input and output below 2 GiB, so that the
+  // out-of-range offset 2^31 lies past both
+  return s.r == 1 && s.s == 1 && s.stride_h == 1 && s.stride_w == 1 && s.pad_h == 0 &&
+         s.pad_w == 0 && pointwise_supported(s.c, g.gemm_n) &&
+         g.gemm_m * s.c < (int64_t(1) << 31) && g.gemm_m * g.gemm_n * 4 < (int64_t(1) << 31);
+}
+
 GemmPlan plan_generic(const i8conv_shape &s, const i8conv_geometry &g) {
   GemmPlan p;
   p.stages = int(ceil_div(g.gemm_k, kStageBytes));
   p.splits = 1;
   p.stages_per_split = p.stages;
+  if (pointwise_eligible(s, g)) {
+    p.pw = true;
+    p.pw_waves = pointwise_waves(g.gemm_m);
+  }
   if (dma_eligible(s)) {
     p.dma = true;
     p.bn = g.gemm_n <= 64 ? 64 : 128;

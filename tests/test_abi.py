@@ -328,6 +328,25 @@ def test_python_layer_raises_on_bad_calls(baseline_cases):
         lab.launch("strip", baseline_cases["cfg3_down_3x3_s2"], FAKE, FAKE, FAKE, FAKE)
 
 
+def test_generic_pointwise_form_eligibility(baseline_cases):
+    # 1x1, stride 1, no padding, C in {64, 128, 256, 512}, N in {32, 64, 128,
+    # 256}, N * C <= 16384: the streaming form, at most 1024 waves
+    d = lab.describe("generic", baseline_cases["cfg4a_pointwise_1x1"])
+    assert "pointwise streaming" in d and "64oc, 1024 waves" in d, d
+    small = lab.ConvShape(1, 1, 1, 128, 64, 1, 1, 0, 0, 1, 1, 1, 1)
+    assert "64oc, 1 waves" in lab.describe("generic", small)
+    for other in (lab.ConvShape(1, 8, 8, 256, 64, 1, 1, 0, 0, 2, 2, 1, 1),   # stride 2
+                  lab.ConvShape(1, 8, 8, 256, 64, 1, 1, 1, 1, 1, 1, 1, 1),   # padded
+                  lab.ConvShape(1, 8, 8, 96, 64, 1, 1, 0, 0, 1, 1, 1, 1),    # C = 96
+                  lab.ConvShape(1, 8, 8, 256, 48, 1, 1, 0, 0, 1, 1, 1, 1),   # N = 48
+                  lab.ConvShape(1, 8, 8, 256, 128, 1, 1, 0, 0, 1, 1, 1, 1),  # N * C > 16384
+                  lab.ConvShape(1, 8, 8, 1024, 32, 1, 1, 0, 0, 1, 1, 1, 1),  # C = 1024
+                  baseline_cases["cfg2_resnet_3x3_s1"]):
+        assert "pointwise" not in lab.describe("generic", other), other
+    # split-K never takes it
+    assert "pointwise" not in lab.describe("splitk", baseline_cases["cfg4a_pointwise_1x1"])
+
+
 def test_pipelined_tile_step_evens_out_the_last_round(baseline_cases):
     # 1568 tiles of 128 pixels leave 32 workgroups for a last round on 256
     # compute units; tiles storing 112 rows give 1792 = 7 * 256.  Grids of

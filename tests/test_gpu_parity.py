@@ -100,6 +100,17 @@ EDGE = {
     "deepk_pad0_m_tail": lab.ConvShape(3, 9, 11, 256, 64, 3, 3, 0, 0, 1, 1, 1, 1),
     "deepk_w1_rows": lab.ConvShape(4, 12, 1, 256, 64, 3, 3, 1, 1, 1, 1, 1, 1),
     "deepk_m512": lab.ConvShape(2, 16, 16, 256, 64, 3, 3, 1, 1, 1, 1, 1, 1),
+    # the generic kernel's pointwise streaming form (1x1, stride 1, no pad):
+    # C = 64 -> 256 channels with a 13-pixel last fragment; C = 512 -> 32
+    # (eight k-steps); 128 -> 128 with a pixel tail; one pixel (one wave of
+    # the grid idle); 2110 fragments, more than one per wave over 1024 waves;
+    # an output above 128 MiB (evict-first stores)
+    "pw_c64_k256_m_tail": lab.ConvShape(3, 7, 9, 64, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_c512_k32": lab.ConvShape(2, 10, 11, 512, 32, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_c128_k128_tail": lab.ConvShape(5, 13, 17, 128, 128, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_one_pixel": lab.ConvShape(1, 1, 1, 128, 64, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_2110_frags": lab.ConvShape(33, 31, 33, 256, 64, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_out_above_128mib": lab.ConvShape(9, 120, 128, 64, 256, 1, 1, 0, 0, 1, 1, 1, 1),
 }
 
 _expected_cache = {}
@@ -218,6 +229,33 @@ def test_int32_accumulator_wraps_like_the_oracle():
             continue
         say(f"[gpu] {kernel} on int32 wrap case")
         assert_bit_exact(run_kernel(kernel, shape, x, w, b), expected, f"{kernel}/wrap")
+
+
+@pytest.mark.gpu
+def test_pointwise_form_falls_back_for_an_unaligned_output():
+    # The pointwise streaming form needs 16-byte aligned pointers: an output
+    # 4 bytes past an allocation's start runs the tile GEMM instead, bit-exact,
+    # and nothing outside the output is written.
+    name = "pw_c128_k128_tail"
+    shape = EDGE[name]
+    assert "pointwise streaming" in lab.describe("generic", shape)
+    x, w, b, expected = _case(name, shape, seed=7)
+    count = shape.geometry().output_elements
+    bufs = [lab.DeviceBuffer.from_array(a) for a in (x, w, b)]
+    yb = lab.DeviceBuffer(4 * count + 16)
+    try:
+        yb.fill(0xA5)
+        say(f"[gpu] generic on {name} with the output at +4 bytes")
+        lab.launch("generic", shape, *bufs, yb.ptr + 4)
+        lab.synchronize()
+        raw = yb.download(np.int32, count + 4)
+    finally:
+        for buf in bufs + [yb]:
+            buf.close()
+    poison = np.uint32(0xA5A5A5A5).view(np.int32)
+    assert raw[0] == poison and np.all(raw[count + 1:] == poison)
+    assert_bit_exact(raw[1:count + 1].reshape(shape.output_shape), expected,
+                     "generic/unaligned output")
 
 
 @pytest.mark.gpu
