@@ -14,7 +14,9 @@ need some tens of ms to bring the clocks to their steady state), between
 two HIP events recorded on the graph's stream behind one more untimed
 replay.  A graph replay begins some microseconds after the previous one
 ends; the timed region holds that gap once, so it weighs on short runs
-(28x28x128: about 0.4 us per launch at K = 20, 0.004 us at K = 2000).
+(28x28x128: about 0.4 us per launch at K = 20, 0.004 us at K = 2000);
+config.stamped_ms_per_step leaves it out (the same launches between
+device clock stamps captured inside the graphs).
 The output is poisoned before those replays and checked against the
 oracle after them.  Beside it: the same K launches enqueued one by one
 on a stream, and the reference's per-launch median (conv_lab.cu:88-110).
@@ -371,6 +373,11 @@ def main() -> int:
                       f"before and checked after the replays",
             "warmup_launches_run": t["warmup_launches"],
             "warmup_ms": round(t["warmup_ms"], 1),
+            # the same K launches from graphs that begin and end with a
+            # clock-stamp kernel: device clock from the first launch's
+            # start to the last one's end, without the gap before the first
+            # replay runs (the kernel's back-to-back rate at any K)
+            "stamped_ms_per_step": round(t["stamped_ms"], 6),
             "stream_ms_per_step": round(stream_ms, 6),
             "per_launch_median_ms": round(median_ms, 6),
             "device": info["arch"],

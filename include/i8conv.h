@@ -255,6 +255,12 @@ typedef struct i8conv_graph_timing {
   int remainder_launches; /* launches of the remainder graph (0: none) */
   int warmup_launches;    /* launches replayed before the timed region */
   float warmup_ms;        /* host wall time of the warmup */
+  /* (end stamp of the last timed graph - start stamp of the first) /
+   * iterations, from the device's constant-rate clock read by a one-wave
+   * kernel captured at the start and at the end of each graph: the timed
+   * launches plus one dispatch, without the gap before the first replay
+   * starts running */
+  float stamped_ms;
 } i8conv_graph_timing;
 
 /* No counterpart in the reference, which times launches one by one
@@ -277,6 +283,12 @@ typedef struct i8conv_graph_timing {
  *      recorded on the stream.  Each graph replay begins with a gap of some
  *      microseconds after the previous one, which the timed region holds
  *      once per replay: a larger L spreads it over more launches.
+ *   8. stamped_ms: the graphs captured again with a clock-stamp kernel
+ *      before the first launch and after the last, one replay to settle,
+ *      then the untimed replay and the timed ones back to back; the time
+ *      runs from the first timed replay's start stamp to the last one's
+ *      end stamp (the launches plus one stamp dispatch, without the gap
+ *      before the first timed replay begins to run).
  * Fills *timing.  Synchronous. */
 int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
                          const int8_t *filter, const int32_t *bias, int32_t *output,

@@ -26,6 +26,20 @@ int hip_fail(const char *what, hipError_t e) {
 bool aligned(const void *p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
+
+// Clock stamps of measure_graph_loop's second pass.  stamps[0] counts the
+// graph replays that have started; replay i's start time goes to
+// stamps[2 + 2 i], its end time to stamps[3 + 2 i] (i < cap; later replays
+// are not recorded).  The time is the device's constant-rate clock
+// (hipDeviceAttributeWallClockRate), read when the kernel's wave runs, that
+// is once the graph's previous node has finished.  One lane, vector atomics
+// and stores.
+__global__ void clock_stamp_kernel(unsigned long long *stamps, int cap, int end) {
+  if (threadIdx.x != 0) return;
+  const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long i = end ? atomicAdd(stamps, 0ull) - 1ull : atomicAdd(stamps, 1ull);
+  if (i < static_cast<unsigned long long>(cap)) stamps[2 + 2 * i + (end ? 1 : 0)] = t;
+}
 // measure() of conv_lab.cu:88-110 around any launch: `warmup` launches,
 // then `iterations` back-to-back launches between one event pair on
 // `stream` (mean per launch: the timed steps follow the warmup directly),
@@ -114,12 +128,25 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
     if (pe == hipSuccess) pe = hipStreamSynchronize(s);
     return pe == hipSuccess ? int(I8CONV_OK) : hip_fail("poison", pe);
   };
-  // captures `count` launches (kernel nodes only) into graphs[slot]
+  // stamped pass: replay records for the untimed replay, the timed main
+  // replays and the remainder
+  const int stamp_cap = full_replays + 2;
+  unsigned long long *stamps = nullptr;
+  // captures `count` launches (kernel nodes only) into graphs[slot]; with
+  // stamps, between a start and an end clock-stamp kernel
   auto capture = [&](int slot, int count) {
     hipError_t ce = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
     if (ce != hipSuccess) return hip_fail("hipStreamBeginCapture", ce);
     int crc = I8CONV_OK;
+    auto stamp = [&](int end) {
+      if (!stamps || crc != I8CONV_OK) return;
+      hipLaunchKernelGGL(clock_stamp_kernel, dim3(1), dim3(64), 0, s, stamps, stamp_cap, end);
+      const hipError_t le = hipGetLastError();
+      if (le != hipSuccess) crc = hip_fail("clock stamp launch", le);
+    };
+    stamp(0);
     for (int i = 0; i < count && crc == I8CONV_OK; ++i) crc = launch(s);
+    stamp(1);
     // end the capture whatever happened inside it
     ce = hipStreamEndCapture(s, &graphs[slot]);
     if (crc == I8CONV_OK && ce != hipSuccess) crc = hip_fail("hipStreamEndCapture", ce);
@@ -177,14 +204,66 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
     timing->warmup_launches = warm_launches;
     timing->warmup_ms = float(warm_ms);
   }
+  auto drop_graphs = [&]() {
+    for (int i = 0; i < 2; ++i) {
+      if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
+      if (graphs[i]) (void)hipGraphDestroy(graphs[i]);
+      execs[i] = nullptr;
+      graphs[i] = nullptr;
+    }
+  };
+  // Second pass, stamped: the same graphs with a clock-stamp kernel at each
+  // end; one replay to settle, the counter cleared, then the untimed replay
+  // and the timed ones back to back; the time runs from the first timed
+  // replay's start stamp to the last one's end stamp.
+  int dev = 0, rate_khz = 0;
+  if (rc == I8CONV_OK && (e = hipGetDevice(&dev)) != hipSuccess) rc = hip_fail("hipGetDevice", e);
+  if (rc == I8CONV_OK &&
+      (e = hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev)) != hipSuccess)
+    rc = hip_fail("hipDeviceGetAttribute(WallClockRate)", e);
+  if (rc == I8CONV_OK && rate_khz <= 0) {
+    set_error("measure_graph: the device reports no wall-clock rate");
+    rc = I8CONV_HIP_ERROR;
+  }
+  const size_t stamp_bytes = sizeof(unsigned long long) * size_t(2 + 2 * stamp_cap);
+  if (rc == I8CONV_OK && (e = hipMalloc(reinterpret_cast<void **>(&stamps), stamp_bytes)) != hipSuccess)
+    rc = hip_fail("hipMalloc(stamps)", e);
+  if (rc == I8CONV_OK) {
+    (void)hipStreamSynchronize(s);
+    drop_graphs();
+    rc = capture(0, per_graph);
+  }
+  if (rc == I8CONV_OK && remainder > 0) rc = capture(1, remainder);
+  if (rc == I8CONV_OK && (e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
+  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("stamped settle", e);
+  std::vector<unsigned long long> host(size_t(2 + 2 * stamp_cap), 0ull);
+  if (rc == I8CONV_OK &&
+      (e = hipMemcpy(stamps, host.data(), stamp_bytes, hipMemcpyHostToDevice)) != hipSuccess)
+    rc = hip_fail("hipMemcpy(stamps)", e);
+  for (int i = 0; i < 1 + full_replays && rc == I8CONV_OK; ++i)
+    if ((e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
+  if (rc == I8CONV_OK && remainder > 0 && (e = hipGraphLaunch(execs[1], s)) != hipSuccess)
+    rc = hip_fail("hipGraphLaunch", e);
+  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("stamped replays", e);
+  if (rc == I8CONV_OK &&
+      (e = hipMemcpy(host.data(), stamps, stamp_bytes, hipMemcpyDeviceToHost)) != hipSuccess)
+    rc = hip_fail("hipMemcpy(stamps)", e);
+  if (rc == I8CONV_OK) {
+    const int last = remainder > 0 ? full_replays + 1 : full_replays;
+    const unsigned long long t0s = host[2 + 2 * 1], t1s = host[3 + 2 * last];
+    if (host[0] != static_cast<unsigned long long>(last + 1) || t1s <= t0s) {
+      set_error("measure_graph: clock stamps out of order");
+      rc = I8CONV_HIP_ERROR;
+    } else {
+      timing->stamped_ms = float(double(t1s - t0s) / (double(rate_khz) * double(iterations)));
+    }
+  }
   // teardown: drain the stream first; a failure here cannot change the result
   (void)hipStreamSynchronize(s);
+  if (stamps) (void)hipFree(stamps);
   if (start) (void)hipEventDestroy(start);
   if (stop) (void)hipEventDestroy(stop);
-  for (int i = 0; i < 2; ++i) {
-    if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
-    if (graphs[i]) (void)hipGraphDestroy(graphs[i]);
-  }
+  drop_graphs();
   (void)hipStreamDestroy(s);
   return rc;
 }

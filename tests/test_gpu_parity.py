@@ -314,6 +314,10 @@ def test_graph_replays_bit_exact(case, baseline_cases):
                                   iterations=iterations, launches_per_graph=per_graph,
                                   min_warmup_ms=1.0, poison_byte=0x5A + call)
             assert t["mean_ms"] > 0
+            # the stamped pass spans the launches and one stamp dispatch, but
+            # not the gap before the first timed replay: positive and no
+            # longer than the event-timed mean plus a few microseconds
+            assert 0 < t["stamped_ms"] < t["mean_ms"] + 0.005
             assert t["launches_per_graph"] == per_graph
             assert t["full_replays"] * per_graph + t["remainder_launches"] == iterations
             assert t["warmup_launches"] >= 2 and t["warmup_ms"] >= 1.0
