@@ -380,7 +380,12 @@ int i8conv_describe(int id, const i8conv_shape *shape, char *buf, size_t len) {
     else
     d = std::string(kNames[id]) +
         (p.pw ? " pointwise streaming: filter in registers, 16px fragments x " +
-                    std::to_string(g.gemm_n) + "oc, " + std::to_string(p.pw_waves) +
+                    std::to_string(g.gemm_n) + "oc" +
+                    (pointwise_slices(shape->c, int(g.gemm_n)) > 1
+                         ? " in " + std::to_string(pointwise_slices(shape->c, int(g.gemm_n))) +
+                               " slices"
+                         : std::string()) +
+                    ", " + std::to_string(p.pw_waves) +
                     " waves; unaligned pointers:"
               : "") +
         (p.dma ? " pipelined" : " register-staged") + " tile " +

@@ -127,13 +127,16 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
                   void *stream);
 // kernel_gemm_dma.hip; splits > 1 writes partial sums to a.partial
 int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stream);
-// kernel_pointwise.hip: C and N with an instance (N / 16 even, C % 64 == 0,
-// N * C <= 16384, C and N powers of two times 64 and 32), its launch, and
-// the pointer alignment it needs (16 bytes each)
-constexpr int kPwWaves = 2;        // waves per workgroup
+// kernel_pointwise.hip: C and N with an instance (C in {64, 128, 256,
+// 512}, N in {32, 64, 128, 256}), the output-channel slices it splits N
+// into (each of 16384 / C channels, at most N), the waves of a launch, its
+// launch, and the pointer alignment it needs (16 bytes each)
 constexpr int kPwMaxWaves = 1024;  // waves per launch, at most
+// waves per workgroup: one per slice, two for one slice
+constexpr int pw_group_waves(int slices) { return slices < 2 ? 2 : slices; }
 bool pointwise_supported(int c, int n);
-int pointwise_waves(int64_t gemm_m);
+int pointwise_slices(int c, int n);
+int pointwise_waves(int64_t gemm_m, int slices);
 int launch_pointwise(const ConvArgs &a, void *stream);
 bool pointwise_pointers_ok(const ConvArgs &a);
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);

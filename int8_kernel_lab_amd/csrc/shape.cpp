@@ -112,18 +112,28 @@ int gemm_dma_step(int64_t gemm_m, int64_t tiles_n, int bm, int bn) {
   return best;
 }
 
-// Pointwise streaming form: instances for N / 16 in {2, 4, 8, 16} and
-// C / 64 in {1, 2, 4, 8} with N * C <= 16384 (the filter as MFMA A operands
-// takes N * C / 1024 VGPRs per lane: at most 64).
+// Pointwise streaming form: instances for C in {64, 128, 256, 512} and N in
+// {32, 64, 128, 256}.  A wave holds a slice of the filter as MFMA A
+// operands, at most 16384 bytes (64 VGPRs per lane): slices of
+// min(N, 16384 / C) output channels, 2 to 8 of them where N * C > 16384.
 bool pointwise_supported(int c, int n) {
   const bool cs = c == 64 || c == 128 || c == 256 || c == 512;
   const bool ns = n == 32 || n == 64 || n == 128 || n == 256;
-  return cs && ns && int64_t(c) * n <= 16384;
+  return cs && ns;
 }
 
-int pointwise_waves(int64_t gemm_m) {
-  const int64_t nfrag = ceil_div(gemm_m, 16);
-  return int(std::min<int64_t>(nfrag, kPwMaxWaves));
+int pointwise_slices(int c, int n) {
+  const int per = std::min(n, 16384 / c);
+  return n / per;
+}
+
+// Two-wave workgroups of one fragment stream each, or one workgroup of SL
+// waves per stream; at most kPwMaxWaves waves (fewer streams than
+// fragments otherwise).
+int pointwise_waves(int64_t gemm_m, int slices) {
+  const int group = pw_group_waves(slices), streams_per_group = group / slices;
+  const int64_t streams = std::min<int64_t>(ceil_div(gemm_m, 16), kPwMaxWaves / slices);
+  return int(ceil_div(streams, streams_per_group) * group);
 }
 
 static bool pointwise_eligible(const i8conv_shape &s, const i8conv_geometry &g) {
@@ -141,7 +151,7 @@ GemmPlan plan_generic(const i8conv_shape &s, const i8conv_geometry &g) {
   p.stages_per_split = p.stages;
   if (pointwise_eligible(s, g)) {
     p.pw = true;
-    p.pw_waves = pointwise_waves(g.gemm_m);
+    p.pw_waves = pointwise_waves(g.gemm_m, pointwise_slices(s.c, int(g.gemm_n)));
   }
   if (dma_eligible(s)) {
     p.dma = true;

@@ -330,16 +330,23 @@ def test_python_layer_raises_on_bad_calls(baseline_cases):
 
 def test_generic_pointwise_form_eligibility(baseline_cases):
     # 1x1, stride 1, no padding, C in {64, 128, 256, 512}, N in {32, 64, 128,
-    # 256}, N * C <= 16384: the streaming form, at most 1024 waves
+    # 256}: the streaming form, at most 1024 waves; where N * C > 16384 the
+    # output channels split into slices of 16384 / C, one wave each
     d = lab.describe("generic", baseline_cases["cfg4a_pointwise_1x1"])
     assert "pointwise streaming" in d and "64oc, 1024 waves" in d, d
     small = lab.ConvShape(1, 1, 1, 128, 64, 1, 1, 0, 0, 1, 1, 1, 1)
-    assert "64oc, 1 waves" in lab.describe("generic", small)
+    assert "64oc, 2 waves" in lab.describe("generic", small)
+    sliced = lab.ConvShape(1, 52, 52, 256, 128, 1, 1, 0, 0, 1, 1, 1, 1)  # 169 fragments
+    assert "128oc in 2 slices, 338 waves" in lab.describe("generic", sliced)
+    big = lab.ConvShape(16, 256, 256, 256, 256, 1, 1, 0, 0, 1, 1, 1, 1)
+    assert "256oc in 4 slices, 1024 waves" in lab.describe("generic", big)
+    c512 = lab.ConvShape(1, 5, 5, 512, 256, 1, 1, 0, 0, 1, 1, 1, 1)
+    assert "256oc in 8 slices, 16 waves" in lab.describe("generic", c512)
     for other in (lab.ConvShape(1, 8, 8, 256, 64, 1, 1, 0, 0, 2, 2, 1, 1),   # stride 2
                   lab.ConvShape(1, 8, 8, 256, 64, 1, 1, 1, 1, 1, 1, 1, 1),   # padded
                   lab.ConvShape(1, 8, 8, 96, 64, 1, 1, 0, 0, 1, 1, 1, 1),    # C = 96
                   lab.ConvShape(1, 8, 8, 256, 48, 1, 1, 0, 0, 1, 1, 1, 1),   # N = 48
-                  lab.ConvShape(1, 8, 8, 256, 128, 1, 1, 0, 0, 1, 1, 1, 1),  # N * C > 16384
+                  lab.ConvShape(1, 8, 8, 256, 512, 1, 1, 0, 0, 1, 1, 1, 1),  # N = 512
                   lab.ConvShape(1, 8, 8, 1024, 32, 1, 1, 0, 0, 1, 1, 1, 1),  # C = 1024
                   baseline_cases["cfg2_resnet_3x3_s1"]):
         assert "pointwise" not in lab.describe("generic", other), other

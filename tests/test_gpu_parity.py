@@ -111,6 +111,13 @@ EDGE = {
     "pw_one_pixel": lab.ConvShape(1, 1, 1, 128, 64, 1, 1, 0, 0, 1, 1, 1, 1),
     "pw_2110_frags": lab.ConvShape(33, 31, 33, 256, 64, 1, 1, 0, 0, 1, 1, 1, 1),
     "pw_out_above_128mib": lab.ConvShape(9, 120, 128, 64, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+    # output channels in slices (one wave each, one fragment stream per
+    # workgroup): 2 slices of 64 with a pixel tail; 8 slices of 32 channels;
+    # 2 slices of 128; 2 slices of 32 over two fragments
+    "pw_slices2_c256_k128": lab.ConvShape(1, 52, 51, 256, 128, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_slices8_c512_k256": lab.ConvShape(3, 10, 10, 512, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_slices2_c128_k256": lab.ConvShape(5, 13, 17, 128, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+    "pw_slices2_c512_k64": lab.ConvShape(1, 3, 7, 512, 64, 1, 1, 0, 0, 1, 1, 1, 1),
 }
 
 _expected_cache = {}
