@@ -174,7 +174,10 @@ int i8conv_requantize(const int32_t *acc, int64_t pixels, int32_t channels,
                       int32_t zero_point, int8_t *output, void *stream);
 /* 1 when the dispatched kernel for `shape` requantizes in its own epilogue
  * (no int32 tensor is written), 0 when the convolution goes through an
- * int32 workspace and a requantizing pass. */
+ * int32 workspace and a requantizing pass.  The generic kernel's pointwise
+ * streaming form (1x1 stride-1 unpadded layers with output-channel slices
+ * of 64 or 128) fuses only when bias, mult, shift and output are 16-byte
+ * aligned; with other pointers its launch needs the unfused workspace. */
 int i8conv_requant_fused(const i8conv_shape *shape);
 /* Workspace i8conv_launch_requant needs: the dispatched kernel's, plus the
  * int32 output (256-byte aligned) when the requantization is not fused. */

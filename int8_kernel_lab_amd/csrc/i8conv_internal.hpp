@@ -137,8 +137,13 @@ constexpr int pw_group_waves(int slices) { return slices < 2 ? 2 : slices; }
 bool pointwise_supported(int c, int n);
 int pointwise_slices(int c, int n);
 int pointwise_waves(int64_t gemm_m, int slices);
-int launch_pointwise(const ConvArgs &a, void *stream);
+// rq: requantized int8 output instead of int32 (needs
+// pointwise_requant_supported and 16-byte aligned mult, shift and output)
+struct RequantArgs;
+int launch_pointwise(const ConvArgs &a, const RequantArgs *rq, void *stream);
 bool pointwise_pointers_ok(const ConvArgs &a);
+// slices of 64 or 128 channels
+bool pointwise_requant_supported(int c, int n);
 int launch_patch(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_halo_resident(const ConvArgs &a, const PatchPlan &p, void *stream);
 int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream);

@@ -309,7 +309,7 @@ int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream) {
   args.partial = nullptr;
   args.splits = 1;
   args.stages_per_split = p.stages;
-  if (p.pw && pointwise_pointers_ok(args)) return launch_pointwise(args, stream);
+  if (p.pw && pointwise_pointers_ok(args)) return launch_pointwise(args, nullptr, stream);
   if (p.dma) return launch_gemm_dma(args, p, 1, stream);
   return launch_any(args, p, 1, static_cast<hipStream_t>(stream));
 }

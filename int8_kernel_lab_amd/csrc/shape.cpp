@@ -127,6 +127,12 @@ int pointwise_slices(int c, int n) {
   return n / per;
 }
 
+bool pointwise_requant_supported(int c, int n) {
+  if (!pointwise_supported(c, n)) return false;
+  const int per = n / pointwise_slices(c, n);
+  return per == 64 || per == 128;
+}
+
 // Two-wave workgroups of one fragment stream each, or one workgroup of SL
 // waves per stream; at most kPwMaxWaves waves (fewer streams than
 // fragments otherwise).

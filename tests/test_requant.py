@@ -108,10 +108,19 @@ def _baseline(name):
     return lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), name)
 
 
-def test_requant_fused_only_for_the_row_kernel_with_copy_waves():
+def test_requant_fused_for_the_row_kernel_with_copy_waves_and_the_pointwise_form():
     assert lab.requant_fused(_baseline("cfg2_resnet_3x3_s1"))
-    for name in ("cfg1_smoke", "cfg3_down_3x3_s2", "cfg4a_pointwise_1x1", "cfg5a_deep_k"):
+    # the generic kernel's pointwise streaming form, slices of 64 channels
+    assert lab.requant_fused(_baseline("cfg4a_pointwise_1x1"))
+    assert lab.requant_workspace_bytes(_baseline("cfg4a_pointwise_1x1")) == 0
+    for name in ("cfg1_smoke", "cfg3_down_3x3_s2", "cfg5a_deep_k"):
         assert not lab.requant_fused(_baseline(name))
+    # pointwise slices of 32 channels (C = 512) or 256 (C = 64, N = 256)
+    # have no requantizing instance
+    for shape in (lab.ConvShape(1, 8, 8, 512, 64, 1, 1, 0, 0, 1, 1, 1, 1),
+                  lab.ConvShape(1, 8, 8, 64, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+                  lab.ConvShape(1, 8, 8, 64, 32, 1, 1, 0, 0, 1, 1, 1, 1)):
+        assert not lab.requant_fused(shape), shape
 
 
 def test_requant_workspace_sizes():
@@ -136,6 +145,12 @@ def test_requant_launch_errors_without_gpu():
     with pytest.raises(lab.I8ConvError) as e:
         lab.requantize(fake, 10, 0, fake, fake, 0, fake)
     assert e.value.status == _lib.BAD_ARGUMENT
+    # the pointwise form fuses only with 16-byte aligned bias, mult, shift
+    # and output; an output at +4 bytes needs the unfused workspace
+    s4a = _baseline("cfg4a_pointwise_1x1")
+    with pytest.raises(lab.I8ConvError, match="16-byte aligned") as e:
+        lab.launch_requant(s4a, fake, fake, fake, fake, fake, 0, fake + 4, None, 0)
+    assert e.value.status == _lib.WORKSPACE_TOO_SMALL
 
 
 # ---- GPU: bit-exact against the oracle --------------------------------------
@@ -215,6 +230,88 @@ def test_fused_requant_edges_bit_exact(name):
     got = lab.conv2d_requant(x, w, b, mult, shift, -20, shape)
     exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, -20)
     np.testing.assert_array_equal(got, exp)
+
+
+POINTWISE_RQ = {
+    # the generic kernel's pointwise form with its requantizing epilogue:
+    # one 64-channel group (whole 128-byte lines of two pixels per store)
+    # with a pixel tail; two groups paired per store; 128-channel slices (2);
+    # 64-channel slices (2 and 4: half-line ordinary stores)
+    "c64_k64_tail": lab.ConvShape(3, 7, 9, 64, 64, 1, 1, 0, 0, 1, 1, 1, 1),
+    "c64_k128": lab.ConvShape(2, 11, 13, 64, 128, 1, 1, 0, 0, 1, 1, 1, 1),
+    "c128_k128_tail": lab.ConvShape(1, 5, 7, 128, 128, 1, 1, 0, 0, 1, 1, 1, 1),
+    "c128_k256_slices2": lab.ConvShape(5, 13, 17, 128, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+    "c256_k128_slices2": lab.ConvShape(1, 52, 51, 256, 128, 1, 1, 0, 0, 1, 1, 1, 1),
+    "c256_k256_slices4": lab.ConvShape(2, 9, 10, 256, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(POINTWISE_RQ))
+def test_pointwise_requant_bit_exact(name):
+    from tests.conftest import say
+    shape = POINTWISE_RQ[name]
+    assert lab.requant_fused(shape), name
+    x, w, b = lab.make_case_data(shape, seed=11)
+    mult, shift = _qparams(shape.k, seed=12)
+    say(f"[gpu] pointwise requant {name} {shape}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, 5, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, 5)
+    np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["c64_k64_tail", "c128_k256_slices2", "c256_k256_slices4",
+                                  "c64_k128"])
+@pytest.mark.parametrize("mixed", [False, True])
+def test_pointwise_requant_short_form_bit_exact(name, mixed):
+    # every channel with shift >= 33: every wave takes the short form; mixed:
+    # one channel of the last slice with shift 32 sends that slice's waves
+    # to the exact form while the others stay short
+    from tests.conftest import say
+    shape = POINTWISE_RQ[name]
+    x, w, b = lab.make_case_data(shape, seed=15)
+    rng = np.random.default_rng(16)
+    mult = (rng.integers(2 ** 30, 2 ** 31, size=shape.k)
+            * rng.choice([-1, 1], size=shape.k)).astype(np.int32)
+    mult[9] = -(2 ** 31)
+    shift = rng.integers(44, 47, size=shape.k).astype(np.int32)
+    if mixed:
+        shift[shape.k - 3] = 32
+    say(f"[gpu] pointwise requant short form {name} mixed={mixed}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, -3, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, -3)
+    assert len(np.unique(exp)) > 200
+    np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.gpu
+def test_pointwise_requant_unaligned_output_takes_the_unfused_path():
+    # output at +4 bytes: the convolution into the int32 workspace and the
+    # requantizing pass, bit-exact, nothing written outside the output
+    from tests.conftest import say
+    shape = POINTWISE_RQ["c64_k128"]
+    x, w, b = lab.make_case_data(shape, seed=13)
+    mult, shift = _qparams(shape.k, seed=14)
+    count = shape.output_elements
+    g = shape.geometry()
+    ws_n = (count * 4 + 255) // 256 * 256 + lab.workspace_bytes(lab.dispatch(shape), shape)
+    bufs = [lab.DeviceBuffer.from_array(a) for a in (x, w, b, mult, shift)]
+    out = lab.DeviceBuffer(count + 32)
+    ws = lab.DeviceBuffer(ws_n)
+    try:
+        out.fill(0x5A)
+        say(f"[gpu] pointwise requant, output at +4 bytes, workspace {ws_n}")
+        lab.launch_requant(shape, *bufs[:3], bufs[3], bufs[4], 5, out.ptr + 4, ws, ws_n)
+        lab.synchronize()
+        raw = out.download(np.int8, count + 32)
+    finally:
+        for buf in bufs + [out, ws]:
+            buf.close()
+    assert g.gemm_m * g.gemm_n == count
+    assert np.all(raw[:4] == 0x5A) and np.all(raw[count + 4:] == 0x5A)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, 5)
+    np.testing.assert_array_equal(raw[4:count + 4].reshape(exp.shape), exp)
 
 
 SHORT_FORM = {
