@@ -33,10 +33,10 @@
 // allow it takes the short form with one 32-bit high multiply per value:
 // the exact form's 64-bit product made the epilogue, not HBM, the limit); a slice needs a multiple of
 // 64 channels, at most 128.  Lane (px, g) then holds, for each group of four
-// channel fragments, four dwords of channels 16 a + 4 g (a = 0..3); four
-// rounds of ds_bpermute among the lanes px, px + 16, px + 32, px + 48
-// transpose them so that the lane holds the 16 contiguous bytes of channels
-// 16 g .. 16 g + 15, and a group is one 16-byte store per lane.  With two
+// channel fragments, four dwords of channels 16 a + 4 g (a = 0..3); two
+// permlane32 and two permlane16 swaps among the lanes px, px + 16, px + 32,
+// px + 48 transpose them so that the lane holds the 16 contiguous bytes of
+// channels 16 g .. 16 g + 15, and a group is one 16-byte store per lane.  With two
 // or four groups per slice, groups are paired by the DPP rotate as above
 // (8 pixels x 128 bytes per store, write-through); a slice of 64 channels
 // alone writes 16 pixels x 64 bytes per store, whole lines when the layer
@@ -187,19 +187,19 @@ __global__ __launch_bounds__(64 * pw_group_waves(SL)) void pointwise_kernel(
             for (int a = 0; a < 4; ++a)
               dq[a] = requant4(acc[4 * h + a], m4[4 * h + a], s4[4 * h + a], zp);
           }
-          // round r: this lane sends dq[(g + r) & 3] and receives, from
-          // lane (px, (g - r) & 3), that lane's dword for fragment g
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int sa = (g + r) & 3, from = (g - r) & 3;
-            const uint32_t send = sa == 0 ? dq[0] : sa == 1 ? dq[1] : sa == 2 ? dq[2] : dq[3];
-            const uint32_t got =
-                r == 0 ? send
-                       : uint32_t(__builtin_amdgcn_ds_bpermute((px + 16 * from) * 4, int(send)));
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (from == j) t[h][j] = int(got);
-          }
+          // 4 x 4 transpose over (row g, dword a) with gfx950's lane swaps:
+          // permlane32_swap(X, Y) exchanges X's rows 2-3 with Y's rows 0-1,
+          // permlane16_swap(X, Y) X's odd rows with Y's even rows (lane
+          // layout checked on the device); afterwards dword j of row g
+          // holds row j's dword g
+          const auto x02 = __builtin_amdgcn_permlane32_swap(dq[0], dq[2], false, false);
+          const auto x13 = __builtin_amdgcn_permlane32_swap(dq[1], dq[3], false, false);
+          const auto y01 = __builtin_amdgcn_permlane16_swap(x02[0], x13[0], false, false);
+          const auto y23 = __builtin_amdgcn_permlane16_swap(x02[1], x13[1], false, false);
+          t[h][0] = int(y01[0]);
+          t[h][1] = int(y01[1]);
+          t[h][2] = int(y23[0]);
+          t[h][3] = int(y23[1]);
         }
         // lane (px, g) holds pixel 16 f + px, channels oc0 + 64 h + 16 g ...
         if constexpr (kGroups == 1) {
