@@ -109,12 +109,20 @@ def copy_calibration(mib: int, steps: int) -> int:
     n = mib * (1 << 20) // 4
     x = torch.ones(n, dtype=torch.int32, device="cuda")
     y = torch.empty_like(x)
+    torch.neg(x, out=y)  # one untimed launch
+    # the launches run on torch's current stream, so torch's events time them
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
     for _ in range(steps):
         torch.neg(x, out=y)
+    stop.record()
     torch.cuda.synchronize()
     assert int(y[0]) == -1 and int(y[-1]) == -1
+    us = start.elapsed_time(stop) * 1e3 / steps
     print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
-                      "launches": steps}), flush=True)
+                      "launches": steps, "us_per_launch": round(us, 3),
+                      "gbps_read_plus_written": round(2 * n * 4 / (us * 1e-6) / 1e9, 1)}),
+          flush=True)
     return 0
 
 
