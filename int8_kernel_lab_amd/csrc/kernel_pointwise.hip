@@ -29,19 +29,19 @@
 //
 // Requantized int8 output (RQ): the same walk with the requantization of
 // kernel_requant.hip (requant4) applied to the accumulators, the filter
-// slice's multipliers and shifts held in VGPRs (a wave whose channels all
-// allow it takes the short form with one 32-bit high multiply per value:
-// the exact form's 64-bit product made the epilogue, not HBM, the limit); a slice needs a multiple of
-// 64 channels, at most 128.  Lane (px, g) then holds, for each group of four
-// channel fragments, four dwords of channels 16 a + 4 g (a = 0..3); two
-// permlane32 and two permlane16 swaps among the lanes px, px + 16, px + 32,
-// px + 48 transpose them so that the lane holds the 16 contiguous bytes of
-// channels 16 g .. 16 g + 15, and a group is one 16-byte store per lane.  With two
-// or four groups per slice, groups are paired by the DPP rotate as above
-// (8 pixels x 128 bytes per store, write-through); a slice of 64 channels
-// alone writes 16 pixels x 64 bytes per store, whole lines when the layer
-// has 64 channels (write-through), half lines otherwise (ordinary stores,
-// merged in the L2).
+// slice's multipliers and shifts held in VGPRs; a wave whose channels all
+// allow it takes the short form (one 32-bit high multiply per value; the
+// exact form's 64-bit product made the epilogue, not HBM, the limit).  A
+// slice needs 64 or 128 channels: one or two groups of four channel
+// fragments.  Lane (px, g) holds, for each group, four dwords of channels
+// 16 a + 4 g (a = 0..3); two permlane32 and two permlane16 swaps among the
+// lanes px, px + 16, px + 32, px + 48 transpose them so that the lane holds
+// the 16 contiguous bytes of channels 16 g .. 16 g + 15, one 16-byte store
+// per lane and group.  Two groups are paired by the DPP rotate as above (8
+// pixels x 128 bytes per store, write-through); a 64-channel slice writes
+// 16 pixels x 64 bytes per store, whole lines when the layer has 64
+// channels (write-through), half lines otherwise (ordinary stores, merged
+// in the L2).
 //
 // Launch shape (measured on config 4a, 64 x 56 x 56 x 256 -> 64): two-wave
 // workgroups, at most 1024 waves (16.4 us per launch; four-wave workgroups
