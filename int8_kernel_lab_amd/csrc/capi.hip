@@ -652,6 +652,14 @@ int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input, const 
   }
   int32_t *acc = static_cast<int32_t *>(workspace);
   void *conv_ws = static_cast<char *>(workspace) + acc_bytes;
+  if (id == I8CONV_KERNEL_SPLITK && g.gemm_n % 4 == 0 && aligned(bias, 16) && aligned(mult, 16) &&
+      aligned(shift, 16) && aligned(output, 4)) {
+    // split-K's second pass requantizes as it adds the splits: the
+    // workspace's int32 output region goes unused
+    const ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
+    const RequantArgs q{mult, shift, zero_point, output};
+    return launch_splitk(args, plan_splitk(*shape, g), conv_ws, stream, &q);
+  }
   const int r = i8conv_launch(id, shape, input, filter, bias, acc, conv_ws,
                               workspace_bytes - acc_bytes, stream);
   if (r != I8CONV_OK) return r;

@@ -122,9 +122,13 @@ ConvArgs make_args(const i8conv_shape &s, const i8conv_geometry &g,
                    int32_t *y);
 
 // Launchers (asynchronous; return an i8conv_status).
+struct RequantArgs;
 int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream);
+// rq: the reduce writes requantized int8 output instead of int32 (needs
+// N % 4 == 0, 16-byte aligned bias, workspace, multipliers and shifts and a
+// 4-byte aligned output)
 int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
-                  void *stream);
+                  void *stream, const RequantArgs *rq = nullptr);
 // kernel_gemm_dma.hip; splits > 1 writes partial sums to a.partial
 int launch_gemm_dma(const ConvArgs &a, const GemmPlan &p, int splits, void *stream);
 // kernel_pointwise.hip: C and N with an instance (C in {64, 128, 256,
@@ -139,7 +143,6 @@ int pointwise_slices(int c, int n);
 int pointwise_waves(int64_t gemm_m, int slices);
 // rq: requantized int8 output instead of int32 (needs
 // pointwise_requant_supported and 16-byte aligned mult, shift and output)
-struct RequantArgs;
 int launch_pointwise(const ConvArgs &a, const RequantArgs *rq, void *stream);
 bool pointwise_pointers_ok(const ConvArgs &a);
 // slices of 64 or 128 channels

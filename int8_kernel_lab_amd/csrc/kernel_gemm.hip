@@ -215,9 +215,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(ConvArgs a) {
 
 // Second pass of split-K: y = bias + partial[0] + partial[1] + ... in split
 // order.  Vector form: four consecutive channels per thread (N % 4 == 0).
+// RQ: the sum requantized (requant4) and stored as four int8 values.
+template <bool RQ>
 __global__ __launch_bounds__(kThreads) void splitk_reduce_vec(
     const int32_t *__restrict__ partial, const int32_t *__restrict__ bias,
-    int32_t *__restrict__ y, int n4, size_t total4, int splits) {
+    int32_t *__restrict__ y, int n4, size_t total4, int splits,
+    const int32_t *__restrict__ mult, const int32_t *__restrict__ shift, int32_t zp,
+    uint32_t *__restrict__ q8) {
   // Each thread walks vec4 items q, q + G, ... (G threads in the grid); its
   // channel group q mod n4 is found once and then advanced by G mod n4,
   // so the loop has no 64-bit division.  The splits are added sixteen
@@ -248,6 +252,13 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_vec(
         for (int u = 0; u < 4; ++u) acc = add_wrap(acc, t[u]);
       }
       for (; sp < splits; ++sp) acc = add_wrap(acc, src[size_t(sp) * total4]);
+      if constexpr (RQ) {
+        q8[q] = requant4(acc, reinterpret_cast<const v4i *>(mult)[c4],
+                         reinterpret_cast<const v4i *>(shift)[c4], zp);
+        c4 += step4;
+        if (c4 >= n4) c4 -= n4;
+        continue;
+      }
       const auto y_r = make_rsrc(reinterpret_cast<v4i *>(y) + qb,
                                  uint32_t(min(size_t(kThreads), total4 - qb)) * 16u);
       store_out4<kStoreThrough>(y_r, uint32_t(threadIdx.x) * 16u, acc);
@@ -315,7 +326,7 @@ int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream) {
 }
 
 int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
-                  void *stream) {
+                  void *stream, const RequantArgs *rq) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   ConvArgs args = a;
   args.partial = static_cast<int32_t *>(workspace);
@@ -334,9 +345,18 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
   size_t blocks = (work + kThreads - 1) / kThreads;
   if (blocks > 4096) blocks = 4096;
   if (blocks == 0) blocks = 1;
-  if (vec) {
-    hipLaunchKernelGGL(splitk_reduce_vec, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
-                       args.partial, a.bias, a.y, a.gemm_n / 4, total / 4, p.splits);
+  if (rq && !vec) {
+    set_error("split-K requantized reduce needs N % 4 == 0 and 16-byte aligned bias and workspace");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  if (rq) {
+    hipLaunchKernelGGL(splitk_reduce_vec<true>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+                       args.partial, a.bias, nullptr, a.gemm_n / 4, total / 4, p.splits, rq->mult,
+                       rq->shift, rq->zero_point, reinterpret_cast<uint32_t *>(rq->y));
+  } else if (vec) {
+    hipLaunchKernelGGL(splitk_reduce_vec<false>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+                       args.partial, a.bias, a.y, a.gemm_n / 4, total / 4, p.splits, nullptr,
+                       nullptr, 0, nullptr);
   } else {
     hipLaunchKernelGGL(splitk_reduce_scalar, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
                        args.partial, a.bias, a.y, a.gemm_n, total, p.splits);

@@ -232,6 +232,30 @@ def test_fused_requant_edges_bit_exact(name):
     np.testing.assert_array_equal(got, exp)
 
 
+SPLITK_RQ = {
+    # split-K's reduce requantizing as it adds the splits (N % 4 == 0): the
+    # deep-channel form with a 4-channel tail past 256; the GEMM form (1x1,
+    # 13x13, C = 1024); N % 4 != 0 takes the int32 pass instead
+    "deepc_k260": lab.ConvShape(4, 5, 9, 4096, 260, 3, 3, 0, 0, 1, 1, 1, 1),
+    "gemm_1x1_13": lab.ConvShape(1, 13, 13, 1024, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+    "k66_pass": lab.ConvShape(1, 7, 7, 2048, 66, 3, 3, 1, 1, 1, 1, 1, 1),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(SPLITK_RQ))
+def test_splitk_requant_bit_exact(name):
+    from tests.conftest import say
+    shape = SPLITK_RQ[name]
+    assert lab.dispatch(shape) == "splitk", name
+    x, w, b = lab.make_case_data(shape, seed=17)
+    mult, shift = _qparams(shape.k, seed=18)
+    say(f"[gpu] split-K requant {name} {shape}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, -9, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, -9)
+    np.testing.assert_array_equal(got, exp)
+
+
 POINTWISE_RQ = {
     # the generic kernel's pointwise form with its requantizing epilogue:
     # one 64-channel group (whole 128-byte lines of two pixels per store)
