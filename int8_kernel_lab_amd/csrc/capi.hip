@@ -660,6 +660,19 @@ int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input, const 
     const RequantArgs q{mult, shift, zero_point, output};
     return launch_splitk(args, plan_splitk(*shape, g), conv_ws, stream, &q);
   }
+  if (id == I8CONV_KERNEL_GENERIC && g.gemm_n % 4 == 0 && aligned(mult, 16) &&
+      aligned(shift, 16) && aligned(output, 4)) {
+    const GemmPlan gp = plan_generic(*shape, g);
+    if (gp.dma) {
+      // the pipelined GEMM's epilogue requantizes: the workspace goes unused
+      ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
+      args.q_mult = mult;
+      args.q_shift = shift;
+      args.q_zp = zero_point;
+      args.q_y = output;
+      return launch_gemm(args, gp, stream);
+    }
+  }
   const int r = i8conv_launch(id, shape, input, filter, bias, acc, conv_ws,
                               workspace_bytes - acc_bytes, stream);
   if (r != I8CONV_OK) return r;

@@ -87,6 +87,13 @@ struct ConvArgs {
   // pipelined GEMM: pixel rows a tile stores (its tile height, or fewer:
   // the tile's last rows then read as zeros and are not stored)
   int m_step;
+  // pipelined GEMM only: requantized int8 output from its epilogue when
+  // q_y != nullptr (y unused), with per-channel multipliers and shifts
+  // (16-byte aligned, N % 4 == 0) and the zero point
+  const int32_t *q_mult;
+  const int32_t *q_shift;
+  int32_t q_zp;
+  int8_t *q_y;
 };
 
 // The lab's int32 -> int8 requantization of one value:

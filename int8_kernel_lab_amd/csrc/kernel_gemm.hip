@@ -320,7 +320,11 @@ int launch_gemm(const ConvArgs &a, const GemmPlan &p, void *stream) {
   args.partial = nullptr;
   args.splits = 1;
   args.stages_per_split = p.stages;
-  if (p.pw && pointwise_pointers_ok(args)) return launch_pointwise(args, nullptr, stream);
+  if (p.pw && !args.q_y && pointwise_pointers_ok(args)) return launch_pointwise(args, nullptr, stream);
+  if (args.q_y && !p.dma) {
+    set_error("requantized GEMM output needs the pipelined kernel (C % 128 == 0)");
+    return I8CONV_BAD_ARGUMENT;
+  }
   if (p.dma) return launch_gemm_dma(args, p, 1, stream);
   return launch_any(args, p, 1, static_cast<hipStream_t>(stream));
 }

@@ -360,8 +360,29 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
       }
     }
   };
+  // Requantized int8 output: a lane's four channels of a pixel as one
+  // 4-byte store (a pixel's 16-channel slice, 16 bytes, per four lanes;
+  // ordinary stores, merged into lines in the L2).
+  auto store_tile_requant = [&]() {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int oc0 = tile_n + wn * TNW + i * 16 + 4 * (lane >> 4);
+      if (oc0 >= a.gemm_n) continue;
+      const v4i m = *reinterpret_cast<const v4i *>(a.q_mult + oc0);
+      const v4i sh = *reinterpret_cast<const v4i *>(a.q_shift + oc0);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
+        if (px >= m_end) continue;
+        *reinterpret_cast<uint32_t *>(a.q_y + size_t(px) * size_t(a.gemm_n) + oc0) =
+            requant4(add_wrap(acc[i][j], bias[i]), m, sh, a.q_zp);
+      }
+    }
+  };
   // one uniform branch for the whole epilogue
-  if (!kSplit && int64_t(a.gemm_m) * a.gemm_n * 4 > kStreamOutputBytes)
+  if (!kSplit && a.q_y)
+    store_tile_requant();
+  else if (!kSplit && int64_t(a.gemm_m) * a.gemm_n * 4 > kStreamOutputBytes)
     store_tile_by_fragment();
   else if (sector_pitch(a.gemm_n))
     store_tile(std::integral_constant<int, kStoreThrough>{});

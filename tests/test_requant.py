@@ -256,6 +256,31 @@ def test_splitk_requant_bit_exact(name):
     np.testing.assert_array_equal(got, exp)
 
 
+GEMM_RQ = {
+    # the pipelined GEMM's requantizing epilogue (C % 128 == 0, N % 4 == 0):
+    # a 1x1 layer whose pointwise form has no requantizing instance (C =
+    # 512); a stride-2 layer with a 4-channel tail past 128; C = 64 takes the
+    # register-staged GEMM and the int32 pass
+    "c512_1x1_k64": lab.ConvShape(1, 9, 9, 512, 64, 1, 1, 0, 0, 1, 1, 1, 1),
+    "s2_k132": lab.ConvShape(8, 28, 28, 128, 132, 3, 3, 1, 1, 2, 2, 1, 1),
+    "c64_s2_pass": lab.ConvShape(2, 16, 16, 64, 64, 3, 3, 1, 1, 2, 2, 1, 1),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(GEMM_RQ))
+def test_gemm_requant_bit_exact(name):
+    from tests.conftest import say
+    shape = GEMM_RQ[name]
+    assert lab.dispatch(shape) == "generic", name
+    x, w, b = lab.make_case_data(shape, seed=19)
+    mult, shift = _qparams(shape.k, seed=20)
+    say(f"[gpu] generic requant {name} {shape}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, 11, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, 11)
+    np.testing.assert_array_equal(got, exp)
+
+
 POINTWISE_RQ = {
     # the generic kernel's pointwise form with its requantizing epilogue:
     # one 64-channel group (whole 128-byte lines of two pixels per store)
