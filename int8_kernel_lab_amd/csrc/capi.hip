@@ -564,8 +564,8 @@ bool fused_requant_plan(const i8conv_shape &s, const i8conv_geometry &g, PatchPl
 // The dispatched plan when it is the generic kernel's pointwise streaming
 // form with a requantizing instance (used when bias, mult, shift and the
 // output are 16-byte aligned).
-bool pointwise_requant_plan(const i8conv_shape &s, const i8conv_geometry &g) {
-  return dispatch(s) == I8CONV_KERNEL_GENERIC && plan_generic(s, g).pw &&
+bool pointwise_requant_plan(const i8conv_shape &s, const i8conv_geometry &g, int id) {
+  return id == I8CONV_KERNEL_GENERIC && plan_generic(s, g).pw &&
          pointwise_requant_supported(s.c, int(g.gemm_n));
 }
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -594,7 +594,9 @@ int i8conv_requant_fused(const i8conv_shape *shape) {
   i8conv_geometry g;
   if (derive(*shape, &g) != I8CONV_OK) return 0;
   PatchPlan pp;
-  return fused_requant_plan(*shape, g, &pp) || pointwise_requant_plan(*shape, g) ? 1 : 0;
+  return fused_requant_plan(*shape, g, &pp) || pointwise_requant_plan(*shape, g, dispatch(*shape))
+             ? 1
+             : 0;
 }
 
 size_t i8conv_requant_workspace_bytes(const i8conv_shape *shape) {
@@ -633,7 +635,7 @@ int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input, const 
     const RequantArgs q{mult, shift, zero_point, output};
     return launch_rowpass(args, pp, stream, &q);
   }
-  if (pointwise_requant_plan(*shape, g) && aligned(bias, 16) && aligned(mult, 16) &&
+  if (pointwise_requant_plan(*shape, g, id) && aligned(bias, 16) && aligned(mult, 16) &&
       aligned(shift, 16) && aligned(output, 16)) {
     // fused: the pointwise form's eligibility keeps the output < 2 GiB
     const ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
@@ -645,7 +647,7 @@ int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input, const 
   if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) {
     set_error("requantized launch needs a 256-byte aligned workspace of " + std::to_string(need) +
               " bytes" +
-              (pointwise_requant_plan(*shape, g)
+              (pointwise_requant_plan(*shape, g, id)
                    ? std::string(" (or bias, mult, shift and output 16-byte aligned)")
                    : std::string()));
     return I8CONV_WORKSPACE_TOO_SMALL;

@@ -24,11 +24,54 @@
 //      every such layer (15.0 vs 18.0 us at 52x52, C = 256);
 //   5. otherwise the generic implicit GEMM (1x1 layers, strided layers,
 //      C % 64 != 0).
+#include <cstring>
+#include <mutex>
+
 #include "i8conv_internal.hpp"
 
 namespace i8conv {
 
+namespace {
+int dispatch_uncached(const i8conv_shape &s);
+
+// The policy is a pure function of the shape, and its planners search
+// (the resident-rows plan of a 64x64 dilated layer takes ~50 us of host
+// time), so results are kept in a small direct-mapped cache: launches that
+// go through the policy every call (the requantized launch, conv2d) then
+// cost a lookup.
+struct DispatchEntry {
+  i8conv_shape shape;
+  int id;
+  bool used;
+};
+constexpr size_t kDispatchCache = 64;
+std::mutex g_dispatch_mutex;
+DispatchEntry g_dispatch_cache[kDispatchCache];
+
+size_t shape_slot(const i8conv_shape &s) {
+  const int *f = reinterpret_cast<const int *>(&s);
+  uint32_t h = 2166136261u;  // FNV-1a over the 13 int fields
+  for (size_t i = 0; i < sizeof(s) / sizeof(int); ++i) h = (h ^ uint32_t(f[i])) * 16777619u;
+  return h % kDispatchCache;
+}
+}  // namespace
+
 int dispatch(const i8conv_shape &s) {
+  static_assert(sizeof(i8conv_shape) == 13 * sizeof(int), "shape fields are 13 ints");
+  const size_t slot = shape_slot(s);
+  {
+    std::lock_guard<std::mutex> lock(g_dispatch_mutex);
+    const DispatchEntry &e = g_dispatch_cache[slot];
+    if (e.used && std::memcmp(&e.shape, &s, sizeof(s)) == 0) return e.id;
+  }
+  const int id = dispatch_uncached(s);
+  std::lock_guard<std::mutex> lock(g_dispatch_mutex);
+  g_dispatch_cache[slot] = DispatchEntry{s, id, true};
+  return id;
+}
+
+namespace {
+int dispatch_uncached(const i8conv_shape &s) {
   i8conv_geometry g;
   if (derive(s, &g) != I8CONV_OK) return -1;
   PatchPlan pp;
@@ -47,5 +90,6 @@ int dispatch(const i8conv_shape &s) {
   }
   return I8CONV_KERNEL_GENERIC;
 }
+}  // namespace
 
 }  // namespace i8conv
