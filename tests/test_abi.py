@@ -366,3 +366,27 @@ def test_pipelined_tile_step_evens_out_the_last_round(baseline_cases):
     assert "stored" not in d and "grid 128x2" in d, d
     # split-K keeps whole tiles
     assert "stored" not in lab.describe("splitk", baseline_cases["cfg5a_deep_k"])
+
+
+def test_dispatch_cache_returns_each_shapes_own_choice():
+    # the policy's results are cached per shape (64 direct-mapped slots):
+    # 300 shapes, many sharing a slot, queried in two different orders give
+    # the same answers as a first pass over them
+    import random
+    rng = random.Random(5)
+    shapes = []
+    for _ in range(300):
+        r = rng.choice([1, 3, 5])
+        shapes.append(lab.ConvShape(rng.randint(1, 8), rng.randint(4, 40), rng.randint(4, 40),
+                                    rng.choice([32, 64, 128, 256, 512, 1024, 2048]),
+                                    rng.choice([16, 36, 64, 128, 256, 512]), r, r,
+                                    r // 2, r // 2, rng.choice([1, 2]), rng.choice([1, 2]),
+                                    rng.choice([1, 2]), 1))
+    first = [lab.dispatch(s) for s in shapes]
+    assert set(first) > {"generic"}
+    order = list(range(len(shapes)))
+    rng.shuffle(order)
+    for i in order:
+        assert lab.dispatch(shapes[i]) == first[i], shapes[i]
+    for i in reversed(range(len(shapes))):
+        assert lab.dispatch(shapes[i]) == first[i], shapes[i]
