@@ -10,13 +10,17 @@ contract, conv_lab.cu:193-194).  Timing (i8conv_measure_graph): the K steps
 are K back-to-back launches captured in one HIP graph (K <= 10000; larger
 K: graphs of 10000 and a remainder), replayed after a warmup of at least W
 launches AND at least --min-warmup-ms of wall time (back-to-back launches
-need some tens of ms to bring the clocks to their steady state), between
-two HIP events recorded on the graph's stream behind one more untimed
-replay.  A graph replay begins some microseconds after the previous one
-ends; the timed region holds that gap once, so it weighs on short runs
-(28x28x128: about 0.4 us per launch at K = 20, 0.004 us at K = 2000);
-config.stamped_ms_per_step leaves it out (the same launches between
-device clock stamps captured inside the graphs).
+need some tens of ms to bring the clocks to their steady state) that ends
+in ~5 ms of replays the host does not wait for: the timed replays are
+enqueued behind them, so the GPU does not idle between the warmup and the
+timed launches (an idle of some hundred microseconds there let the first
+launches after it run ~10 % slower).  The time is taken between two HIP
+events recorded on the graph's stream.  A graph replay begins some
+microseconds after the previous one ends; the timed region holds that gap
+once per replay, so it weighs on short runs (28x28x128: about 0.4 us per
+launch at K = 20, 0.004 us at K = 2000); config.stamped_ms_per_step leaves
+it out (the same launches from graphs that begin and end with a device
+clock-stamp kernel, replayed right before the event-timed ones).
 The output is poisoned before those replays and checked against the
 oracle after them.  Beside it: the same K launches enqueued one by one
 on a stream, and the reference's per-launch median (conv_lab.cu:88-110).
@@ -376,9 +380,10 @@ def main() -> int:
             "algorithmic_bytes_per_step": nbytes,
             "pct_int8_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
             "timing": f"{args.steps} back-to-back launches timed as {graphs}, after "
-                      f"{t['warmup_launches']} warmup launches over {t['warmup_ms']:.0f} ms and one "
-                      f"untimed replay in flight at the start event; output poisoned "
-                      f"before and checked after the replays",
+                      f"{t['warmup_launches']} warmup launches over {t['warmup_ms']:.0f} ms, the "
+                      f"last ~5 ms of them enqueued with the timed replays behind them (no idle "
+                      f"GPU between warmup and timing); output poisoned before and checked "
+                      f"after the replays",
             "warmup_launches_run": t["warmup_launches"],
             "warmup_ms": round(t["warmup_ms"], 1),
             # the same K launches from graphs that begin and end with a
@@ -386,6 +391,7 @@ def main() -> int:
             # start to the last one's end, without the gap before the first
             # replay runs (the kernel's back-to-back rate at any K)
             "stamped_ms_per_step": round(t["stamped_ms"], 6),
+            "stream_behind_warm_ms_per_step": round(t["stream_ms"], 6),
             "stream_ms_per_step": round(stream_ms, 6),
             "per_launch_median_ms": round(median_ms, 6),
             "device": info["arch"],

@@ -174,13 +174,18 @@ int i8conv_requantize(const int32_t *acc, int64_t pixels, int32_t channels,
                       int32_t zero_point, int8_t *output, void *stream);
 /* 1 when the dispatched kernel for `shape` requantizes in its own epilogue
  * (no int32 tensor is written), 0 when the convolution goes through an
- * int32 workspace and a requantizing pass.  The generic kernel's pointwise
- * streaming form (1x1 stride-1 unpadded layers with output-channel slices
- * of 64 or 128) fuses only when bias, mult, shift and output are 16-byte
- * aligned; with other pointers its launch needs the unfused workspace. */
+ * int32 workspace and a requantizing pass.  Fused: the row kernel with
+ * copy waves; the generic kernel's pointwise streaming form (1x1 stride-1
+ * unpadded layers with output-channel slices of 64 or 128), when bias,
+ * mult, shift and output are 16-byte aligned; split-K's second pass (N % 4
+ * == 0), when bias, mult and shift are 16-byte aligned; the pipelined GEMM's
+ * epilogue (N % 4 == 0), when mult and shift are 16-byte aligned.  With
+ * other pointers the launch takes the unfused way, whose workspace is the
+ * int32 output plus the kernel's own. */
 int i8conv_requant_fused(const i8conv_shape *shape);
-/* Workspace i8conv_launch_requant needs: the dispatched kernel's, plus the
- * int32 output (256-byte aligned) when the requantization is not fused. */
+/* Workspace i8conv_launch_requant needs: the dispatched kernel's own (split-K's
+ * partial sums; nothing for the other kernels), plus the int32 output
+ * (256-byte aligned) when the requantization is not fused. */
 size_t i8conv_requant_workspace_bytes(const i8conv_shape *shape);
 /* The dispatched convolution with int8 output: fused epilogue or
  * convolution into the workspace + requantizing pass.  Allocates nothing. */
@@ -245,6 +250,17 @@ int i8conv_stream_destroy(void *stream);
  * clears it. */
 int i8conv_wait_expired(int *expired);
 
+/* No counterpart in the reference: a test hook for the give-up path above.
+ * Sets the polls each bounded wait makes before it gives up, for launches
+ * enqueued from then on (the value is read at launch, so a captured graph
+ * keeps the limit of its capture).  Default 2^20 (some tens of ms); 0 makes
+ * every wait give up at once: every wave still runs to its end, the output
+ * is then wrong and i8conv_wait_expired reports it.  polls < 0 is rejected.
+ * Process-wide, not per thread. */
+int i8conv_set_wait_spin_limit(int polls);
+/* The current limit (i8conv_set_wait_spin_limit). */
+int i8conv_wait_spin_limit(void);
+
 /* Device facts for roofline reporting: compute units, peak engine clock in
  * kHz, gcnArchName (at most `name_len` bytes incl. NUL). */
 int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
@@ -264,34 +280,44 @@ typedef struct i8conv_graph_timing {
    * launches plus one dispatch, without the gap before the first replay
    * starts running */
   float stamped_ms;
+  /* the same K launches enqueued one by one on the stream (no graph),
+   * between one pair of events, right after the stamped region: elapsed /
+   * iterations */
+  float stream_ms;
 } i8conv_graph_timing;
 
 /* No counterpart in the reference, which times launches one by one
  * (conv_lab.cu:88-110).  Back-to-back launches replayed from HIP graphs, on
  * a stream of its own (default priority):
  *   1. one launch outside any graph, synchronized;
- *   2. when poison_byte >= 0, the output is filled with that byte (outside
- *      any graph, synchronous);
- *   3. a main graph of L = min(launches_per_graph, iterations)
- *      i8conv_launch calls is captured (kernel nodes only), and a
- *      remainder graph of iterations % L launches when that is nonzero;
- *   4. warmup: main-graph replays until at least `warmup` launches have run
- *      and at least min_warmup_ms of host wall time has passed;
- *   5. the output is poisoned again (step 2), so that it then holds only
- *      what graph replays wrote;
- *   6. one more main-graph replay, untimed and not waited for, so that the
- *      timed launches start behind running ones;
- *   7. timed region: iterations / L main-graph replays plus the remainder
- *      graph, exactly `iterations` launches, between one pair of events
- *      recorded on the stream.  Each graph replay begins with a gap of some
- *      microseconds after the previous one, which the timed region holds
- *      once per replay: a larger L spreads it over more launches.
- *   8. stamped_ms: the graphs captured again with a clock-stamp kernel
- *      before the first launch and after the last, one replay to settle,
- *      then the untimed replay and the timed ones back to back; the time
- *      runs from the first timed replay's start stamp to the last one's
- *      end stamp (the launches plus one stamp dispatch, without the gap
- *      before the first timed replay begins to run).
+ *   2. graphs of L = min(launches_per_graph, iterations) i8conv_launch
+ *      calls are captured (kernel nodes only), plus a remainder graph of
+ *      iterations % L launches when that is nonzero: a plain pair and a
+ *      stamped pair, whose graphs begin and end with a one-wave kernel
+ *      that reads the device's constant-rate clock;
+ *   3. warmup: main-graph replays, in batches the host waits for, until at
+ *      least `warmup` launches have run and at least min_warmup_ms of host
+ *      wall time has passed;
+ *   4. a tail of about 5 ms of main-graph replays that the host does not
+ *      wait for; steps 5-7 are enqueued behind it, so the GPU goes from
+ *      warm launches into the timed ones without idling;
+ *   5. stamped region: the K launches from the stamped graphs; stamped_ms
+ *      runs from the first graph's start stamp to the last one's end stamp
+ *      (the launches plus one stamp dispatch, without the gap before each
+ *      graph replay begins to run);
+ *   5b. stream region: the K launches enqueued one by one on the stream
+ *      (not from a graph) between one pair of events (stream_ms); they are
+ *      enqueued while the tail still runs, so the GPU does not wait for
+ *      the host;
+ *   6. when poison_byte >= 0, the output is filled with that byte (a fill
+ *      on the stream, outside any graph), so that it then holds only what
+ *      the event-timed replays wrote;
+ *   7. event-timed region: iterations / L main-graph replays plus the
+ *      remainder graph, exactly `iterations` launches, between one pair of
+ *      events recorded on the stream (mean_ms).  Each graph replay begins
+ *      with a gap of some microseconds after the previous one, which the
+ *      region holds once per replay: a larger L spreads it over more
+ *      launches.
  * Fills *timing.  Synchronous. */
 int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
                          const int8_t *filter, const int32_t *bias, int32_t *output,

@@ -38,6 +38,7 @@ __all__ = [
     "synchronize", "requantize", "requant_fused", "requant_workspace_bytes", "launch_requant",
     "conv2d_requant", "measure_requant", "nchw_to_nhwc", "nhwc_to_nchw", "nhwk_to_nkhw",
     "pack_vect_c", "unpack_vect_c", "measure_graph", "measure_store_floor", "measure_lds_probe", "wait_expired", "launch_noalloc",
+    "set_wait_spin_limit", "wait_spin_limit", "DEFAULT_WAIT_SPIN_LIMIT",
 ]
 
 KERNELS = ("generic", "strip", "halo", "splitk")
@@ -402,13 +403,28 @@ def lds_probe_expected(pattern: str, threads: int, reads_per_lane: int):
 
 
 def wait_expired() -> bool:
-    """True when a row-kernel wave's bounded wait gave up since the last call
-    (i8conv_wait_expired: synchronizes the device, reads and clears the
-    word); the outputs of the launches since then are then not to be
-    trusted."""
+    """True when a bounded wait (row kernel with copy waves or deep-channel
+    split-K) gave up since the last call (i8conv_wait_expired: synchronizes
+    the device, reads and clears the word); the outputs of the launches
+    since then are then not to be trusted."""
     flag = ctypes.c_int()
     check(lib().i8conv_wait_expired(ctypes.byref(flag)), "wait_expired")
     return bool(flag.value)
+
+
+DEFAULT_WAIT_SPIN_LIMIT = 1 << 20
+
+
+def set_wait_spin_limit(polls: int) -> None:
+    """Test hook for the give-up path (i8conv_set_wait_spin_limit): the polls
+    each bounded wait of later launches makes before it gives up; 0 makes
+    every wait give up at once (the launch then runs to its end with a wrong
+    output that wait_expired() reports)."""
+    check(lib().i8conv_set_wait_spin_limit(int(polls)), "set_wait_spin_limit")
+
+
+def wait_spin_limit() -> int:
+    return int(lib().i8conv_wait_spin_limit())
 
 
 def device_info() -> Dict[str, object]:
@@ -459,6 +475,9 @@ def conv2d(input: np.ndarray, filter: np.ndarray, bias: np.ndarray, shape: ConvS
     try:
         launch(name, shape, xb, wb, bb, yb, ws, ws_n)
         synchronize()
+        if wait_expired():
+            raise I8ConvError(_lib.HIP_ERROR, f"conv2d ({name}): a bounded wait gave up "
+                              "during the launch; its output is not to be trusted")
         return yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
     finally:
         for b in (xb, wb, bb, yb, ws):
@@ -510,6 +529,9 @@ def conv2d_requant(input: np.ndarray, filter: np.ndarray, bias: np.ndarray, mult
     try:
         launch_requant(shape, *bufs[:5], zero_point, yb, ws, ws_n)
         synchronize()
+        if wait_expired():
+            raise I8ConvError(_lib.HIP_ERROR, "conv2d_requant: a bounded wait gave up during "
+                              "the launch; its output is not to be trusted")
         return yb.download(np.int8, g.output_elements).reshape(shape.output_shape)
     finally:
         for b in bufs + [yb, ws]:

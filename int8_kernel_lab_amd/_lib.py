@@ -46,7 +46,8 @@ class CGraphTiming(ctypes.Structure):
 
     _fields_ = [("mean_ms", c_float), ("launches_per_graph", c_int), ("full_replays", c_int),
                 ("remainder_launches", c_int), ("warmup_launches", c_int),
-                ("warmup_ms", c_float), ("stamped_ms", c_float)]
+                ("warmup_ms", c_float), ("stamped_ms", c_float),
+                ("stream_ms", c_float)]
 
 
 # name -> (restype, argtypes); every symbol include/i8conv.h declares.
@@ -99,6 +100,8 @@ SIGNATURES = {
     "i8conv_stream_create": (c_int, [POINTER(c_void_p)]),
     "i8conv_stream_destroy": (c_int, [c_void_p]),
     "i8conv_wait_expired": (c_int, [POINTER(c_int)]),
+    "i8conv_set_wait_spin_limit": (c_int, [c_int]),
+    "i8conv_wait_spin_limit": (c_int, []),
     "i8conv_device_info": (c_int, [POINTER(c_int), POINTER(c_int), c_char_p, c_size_t]),
     "i8conv_measure_graph": (c_int, [c_int, POINTER(CShape), c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_size_t, c_int, c_double, c_int,

@@ -3,7 +3,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
+#include <cmath>
 #include <initializer_list>
 #include <mutex>
 #include <string>
@@ -27,8 +29,8 @@ bool aligned(const void *p, uintptr_t a) {
   return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }
 
-// Clock stamps of measure_graph_loop's second pass.  stamps[0] counts the
-// graph replays that have started; replay i's start time goes to
+// Clock stamps of measure_graph_loop's stamped region.  stamps[0] counts
+// the stamped graph replays that have started; replay i's start time goes to
 // stamps[2 + 2 i], its end time to stamps[3 + 2 i] (i < cap; later replays
 // are not recorded).  The time is the device's constant-rate clock
 // (hipDeviceAttributeWallClockRate), read when the kernel's wave runs, that
@@ -42,9 +44,9 @@ __global__ void clock_stamp_kernel(unsigned long long *stamps, int cap, int end)
 }
 // measure() of conv_lab.cu:88-110 around any launch: `warmup` launches,
 // then `iterations` back-to-back launches between one event pair on
-// `stream` (mean per launch: the timed steps follow the warmup directly),
-// then `iterations` launches each bracketed by its own event pair and
-// synchronized (median per launch).
+// `stream` (mean per launch: the timed steps are enqueued right behind the
+// warmup, with no synchronization between), then `iterations` launches each
+// bracketed by its own event pair and synchronized (median per launch).
 template <class Launch>
 int measure_loop(Launch launch, void *stream, int warmup, int iterations, float *median_ms,
                  float *batched_ms) {
@@ -57,8 +59,11 @@ int measure_loop(Launch launch, void *stream, int warmup, int iterations, float 
     const int rc = launch();
     if (rc != I8CONV_OK) return rc;
   }
-  hipError_t e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return hip_fail("warmup", e);
+  hipError_t e = hipSuccess;
+  // without the batched figure the warmup is synchronized here; with it,
+  // the batched launches are enqueued right behind the warmup (the GPU
+  // does not idle before them) and synchronized after
+  if (!batched_ms && (e = hipStreamSynchronize(s)) != hipSuccess) return hip_fail("warmup", e);
   hipEvent_t start, stop;
   if ((e = hipEventCreate(&start)) != hipSuccess) return hip_fail("hipEventCreate", e);
   if ((e = hipEventCreate(&stop)) != hipSuccess) {
@@ -97,14 +102,18 @@ int measure_loop(Launch launch, void *stream, int warmup, int iterations, float 
 }
 
 // Back-to-back launches replayed from HIP graphs on a stream of its own
-// (default priority), the steps documented at i8conv_measure_graph: the
-// main graph is replayed between host-recorded events (one untimed replay
-// first, so that the timed ones start behind running work) and a remainder
-// graph completes the count.  Each graph replay starts some microseconds
-// after the previous one ends (28x28x128: ~8 us), so the timed region
+// (default priority), the steps documented at i8conv_measure_graph.  The
+// warmup ends in a tail of replays that the host does not wait for, and
+// both timed regions are enqueued behind it: the timed launches run on a
+// GPU that has not idled since the warmup (an idle of some hundred
+// microseconds while the host synchronizes, poisons the output and records
+// events let the first launches after it run ~10 % slower on 28x28x128,
+// which weighed on short runs).  Each graph replay starts some microseconds
+// after the previous one ends (28x28x128: ~8 us), so the event-timed region
 // holds one such gap per replay; event records captured into a graph would
 // keep it out, but HIP cannot time them (hipEventElapsedTime fails on
-// them).  launch(stream) enqueues one launch.
+// them), hence the stamped figure beside it.  launch(stream) enqueues one
+// launch.
 template <class Launch>
 int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup,
                        double min_warmup_ms, int iterations, int launches_per_graph,
@@ -112,34 +121,37 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   const int per_graph = std::min(launches_per_graph, iterations);
   const int full_replays = iterations / per_graph;
   const int remainder = iterations - full_replays * per_graph;
+  const int replays = full_replays + (remainder > 0 ? 1 : 0);
   *timing = i8conv_graph_timing{};
 
   hipStream_t s = nullptr;
   hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);  // default priority
   if (e != hipSuccess) return hip_fail("hipStreamCreateWithFlags", e);
-  hipGraph_t graphs[2] = {nullptr, nullptr};
-  hipGraphExec_t execs[2] = {nullptr, nullptr};
-  hipEvent_t start = nullptr, stop = nullptr;
-  // poisons the output outside any graph (synchronous), so that a check
-  // after the replays sees only what the replays wrote
+  // graphs: [0] main, [1] remainder, [2] stamped main, [3] stamped remainder
+  hipGraph_t graphs[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipGraphExec_t execs[4] = {nullptr, nullptr, nullptr, nullptr};
+  hipEvent_t start = nullptr, stop = nullptr, sstart = nullptr, sstop = nullptr;
+  // fills the output with the poison byte, enqueued on the stream (a fill
+  // kernel outside any graph), so that a check after the event-timed
+  // replays sees only what they wrote
   auto poison = [&]() {
     if (poison_byte < 0 || out_bytes == 0) return int(I8CONV_OK);
-    hipError_t pe = hipMemsetAsync(output, poison_byte, out_bytes, s);
-    if (pe == hipSuccess) pe = hipStreamSynchronize(s);
+    const hipError_t pe = hipMemsetAsync(output, poison_byte, out_bytes, s);
     return pe == hipSuccess ? int(I8CONV_OK) : hip_fail("poison", pe);
   };
-  // stamped pass: replay records for the untimed replay, the timed main
-  // replays and the remainder
-  const int stamp_cap = full_replays + 2;
+  // stamped replays: one record each (start, end)
+  const int stamp_cap = replays;
+  const size_t stamp_bytes = sizeof(unsigned long long) * size_t(2 + 2 * stamp_cap);
   unsigned long long *stamps = nullptr;
-  // captures `count` launches (kernel nodes only) into graphs[slot]; with
-  // stamps, between a start and an end clock-stamp kernel
+  // captures `count` launches (kernel nodes only) into graphs[slot]; the
+  // stamped slots (2, 3) between a start and an end clock-stamp kernel
   auto capture = [&](int slot, int count) {
+    const bool stamped = slot >= 2;
     hipError_t ce = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
     if (ce != hipSuccess) return hip_fail("hipStreamBeginCapture", ce);
     int crc = I8CONV_OK;
     auto stamp = [&](int end) {
-      if (!stamps || crc != I8CONV_OK) return;
+      if (!stamped || crc != I8CONV_OK) return;
       hipLaunchKernelGGL(clock_stamp_kernel, dim3(1), dim3(64), 0, s, stamps, stamp_cap, end);
       const hipError_t le = hipGetLastError();
       if (le != hipSuccess) crc = hip_fail("clock stamp launch", le);
@@ -155,68 +167,21 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
       crc = hip_fail("hipGraphInstantiate", ce);
     return crc;
   };
+  // enqueues the K timed launches from graph slots base (main) and base + 1
+  auto replay_all = [&](int base) {
+    for (int i = 0; i < full_replays; ++i)
+      if (const hipError_t ge = hipGraphLaunch(execs[base], s); ge != hipSuccess)
+        return hip_fail("hipGraphLaunch", ge);
+    if (remainder > 0)
+      if (const hipError_t ge = hipGraphLaunch(execs[base + 1], s); ge != hipSuccess)
+        return hip_fail("hipGraphLaunch", ge);
+    return int(I8CONV_OK);
+  };
+  int dev = 0, rate_khz = 0;
   // one launch outside the graphs (checks the arguments, sets any function
-  // attribute the kernel needs), then the poison, then the captures
+  // attribute the kernel needs), then the captures
   int rc = launch(s);
   if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("launch", e);
-  if (rc == I8CONV_OK) rc = poison();
-  if (rc == I8CONV_OK && (e = hipEventCreate(&start)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
-  if (rc == I8CONV_OK && (e = hipEventCreate(&stop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
-  if (rc == I8CONV_OK) rc = capture(0, per_graph);
-  if (rc == I8CONV_OK && remainder > 0) rc = capture(1, remainder);
-  // warmup: replays of the main graph until at least `warmup` launches have
-  // run and at least min_warmup_ms of wall time has passed (back-to-back
-  // launches need some tens of ms to bring the clocks to their steady
-  // state); batches of replays between host checks, doubling up to 64
-  int warm_launches = 0;
-  double warm_ms = 0.0;
-  const auto t0 = std::chrono::steady_clock::now();
-  for (int batch = 1; rc == I8CONV_OK && (warm_launches < warmup || warm_ms < min_warmup_ms);) {
-    for (int i = 0; i < batch && rc == I8CONV_OK; ++i)
-      if ((e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
-    if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("warmup", e);
-    warm_launches += batch * per_graph;
-    warm_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
-                  .count();
-    batch = std::min(2 * batch, 64);
-  }
-  if (rc == I8CONV_OK) rc = poison();
-  // one untimed replay, enqueued without a synchronization, so that the
-  // start event is recorded behind running launches
-  if (rc == I8CONV_OK && (e = hipGraphLaunch(execs[0], s)) != hipSuccess)
-    rc = hip_fail("hipGraphLaunch", e);
-  // the timed region: exactly `iterations` launches
-  if (rc == I8CONV_OK && (e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-  for (int i = 0; i < full_replays && rc == I8CONV_OK; ++i)
-    if ((e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
-  if (rc == I8CONV_OK && remainder > 0 && (e = hipGraphLaunch(execs[1], s)) != hipSuccess)
-    rc = hip_fail("hipGraphLaunch", e);
-  if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("hipStreamSynchronize", e);
-  float ms = 0.f;
-  if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess)
-    rc = hip_fail("hipEventElapsedTime", e);
-  if (rc == I8CONV_OK) {
-    timing->mean_ms = ms / float(iterations);
-    timing->launches_per_graph = per_graph;
-    timing->full_replays = full_replays;
-    timing->remainder_launches = remainder;
-    timing->warmup_launches = warm_launches;
-    timing->warmup_ms = float(warm_ms);
-  }
-  auto drop_graphs = [&]() {
-    for (int i = 0; i < 2; ++i) {
-      if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
-      if (graphs[i]) (void)hipGraphDestroy(graphs[i]);
-      execs[i] = nullptr;
-      graphs[i] = nullptr;
-    }
-  };
-  // Second pass, stamped: the same graphs with a clock-stamp kernel at each
-  // end; one replay to settle, the counter cleared, then the untimed replay
-  // and the timed ones back to back; the time runs from the first timed
-  // replay's start stamp to the last one's end stamp.
-  int dev = 0, rate_khz = 0;
   if (rc == I8CONV_OK && (e = hipGetDevice(&dev)) != hipSuccess) rc = hip_fail("hipGetDevice", e);
   if (rc == I8CONV_OK &&
       (e = hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev)) != hipSuccess)
@@ -225,37 +190,90 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
     set_error("measure_graph: the device reports no wall-clock rate");
     rc = I8CONV_HIP_ERROR;
   }
-  const size_t stamp_bytes = sizeof(unsigned long long) * size_t(2 + 2 * stamp_cap);
   if (rc == I8CONV_OK && (e = hipMalloc(reinterpret_cast<void **>(&stamps), stamp_bytes)) != hipSuccess)
     rc = hip_fail("hipMalloc(stamps)", e);
-  if (rc == I8CONV_OK) {
-    (void)hipStreamSynchronize(s);
-    drop_graphs();
-    rc = capture(0, per_graph);
-  }
+  if (rc == I8CONV_OK && (e = hipEventCreate(&start)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&stop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&sstart)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&sstop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK) rc = capture(0, per_graph);
   if (rc == I8CONV_OK && remainder > 0) rc = capture(1, remainder);
-  if (rc == I8CONV_OK && (e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
-  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("stamped settle", e);
-  std::vector<unsigned long long> host(size_t(2 + 2 * stamp_cap), 0ull);
-  if (rc == I8CONV_OK &&
-      (e = hipMemcpy(stamps, host.data(), stamp_bytes, hipMemcpyHostToDevice)) != hipSuccess)
-    rc = hip_fail("hipMemcpy(stamps)", e);
-  for (int i = 0; i < 1 + full_replays && rc == I8CONV_OK; ++i)
+  if (rc == I8CONV_OK) rc = capture(2, per_graph);
+  if (rc == I8CONV_OK && remainder > 0) rc = capture(3, remainder);
+  // warmup: replays of the main graph until at least `warmup` launches have
+  // run and at least min_warmup_ms of wall time has passed (back-to-back
+  // launches need some tens of ms to bring the clocks to their steady
+  // state); batches of replays between host checks, doubling up to 64
+  int warm_launches = 0;
+  double warm_ms = 0.0, batch_ms = 0.0;
+  int last_batch = 1;
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int batch = 1; rc == I8CONV_OK && (warm_launches < warmup || warm_ms < min_warmup_ms);) {
+    const auto b0 = std::chrono::steady_clock::now();
+    for (int i = 0; i < batch && rc == I8CONV_OK; ++i)
+      if ((e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
+    if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("warmup", e);
+    const auto b1 = std::chrono::steady_clock::now();
+    warm_launches += batch * per_graph;
+    warm_ms = std::chrono::duration<double, std::milli>(b1 - t0).count();
+    batch_ms = std::chrono::duration<double, std::milli>(b1 - b0).count();
+    last_batch = batch;
+    batch = std::min(2 * batch, 64);
+  }
+  // The tail: about kTailMs of main-graph replays (by the last batch's
+  // rate, at least one and at most 4096), not waited for; everything after
+  // it is enqueued while it runs, so the GPU goes from warm launches
+  // straight into the timed ones.
+  constexpr double kTailMs = 5.0;
+  const double ms_per_replay = batch_ms / double(last_batch);
+  const int tail = ms_per_replay > 0.0
+                       ? int(std::min(4096.0, std::max(1.0, std::ceil(kTailMs / ms_per_replay))))
+                       : 1;
+  for (int i = 0; i < tail && rc == I8CONV_OK; ++i)
     if ((e = hipGraphLaunch(execs[0], s)) != hipSuccess) rc = hip_fail("hipGraphLaunch", e);
-  if (rc == I8CONV_OK && remainder > 0 && (e = hipGraphLaunch(execs[1], s)) != hipSuccess)
-    rc = hip_fail("hipGraphLaunch", e);
-  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("stamped replays", e);
+  if (rc == I8CONV_OK) warm_launches += tail * per_graph;
+  // stamped region: the stamp records cleared on the stream, then the K
+  // launches from the stamped graphs
+  if (rc == I8CONV_OK && (e = hipMemsetAsync(stamps, 0, stamp_bytes, s)) != hipSuccess)
+    rc = hip_fail("hipMemsetAsync(stamps)", e);
+  if (rc == I8CONV_OK) rc = replay_all(2);
+  // stream region: the K launches enqueued one by one on the stream, not
+  // from a graph, between one pair of events (enqueued while the tail
+  // still runs, so the GPU does not wait for the host)
+  if (rc == I8CONV_OK && (e = hipEventRecord(sstart, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch(s);
+  if (rc == I8CONV_OK && (e = hipEventRecord(sstop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  // event-timed region: the output poisoned, then exactly `iterations`
+  // launches between one pair of events
+  if (rc == I8CONV_OK) rc = poison();
+  if (rc == I8CONV_OK && (e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  if (rc == I8CONV_OK) rc = replay_all(0);
+  if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("hipStreamSynchronize", e);
+  float ms = 0.f, sms = 0.f;
+  if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess)
+    rc = hip_fail("hipEventElapsedTime", e);
+  if (rc == I8CONV_OK && (e = hipEventElapsedTime(&sms, sstart, sstop)) != hipSuccess)
+    rc = hip_fail("hipEventElapsedTime", e);
+  std::vector<unsigned long long> host(size_t(2 + 2 * stamp_cap), 0ull);
   if (rc == I8CONV_OK &&
       (e = hipMemcpy(host.data(), stamps, stamp_bytes, hipMemcpyDeviceToHost)) != hipSuccess)
     rc = hip_fail("hipMemcpy(stamps)", e);
   if (rc == I8CONV_OK) {
-    const int last = remainder > 0 ? full_replays + 1 : full_replays;
-    const unsigned long long t0s = host[2 + 2 * 1], t1s = host[3 + 2 * last];
-    if (host[0] != static_cast<unsigned long long>(last + 1) || t1s <= t0s) {
+    const int last = replays - 1;
+    const unsigned long long t0s = host[2], t1s = host[3 + 2 * last];
+    if (host[0] != static_cast<unsigned long long>(replays) || t1s <= t0s) {
       set_error("measure_graph: clock stamps out of order");
       rc = I8CONV_HIP_ERROR;
     } else {
+      timing->mean_ms = ms / float(iterations);
+      timing->launches_per_graph = per_graph;
+      timing->full_replays = full_replays;
+      timing->remainder_launches = remainder;
+      timing->warmup_launches = warm_launches;
+      timing->warmup_ms = float(warm_ms);
       timing->stamped_ms = float(double(t1s - t0s) / (double(rate_khz) * double(iterations)));
+      timing->stream_ms = sms / float(iterations);
     }
   }
   // teardown: drain the stream first; a failure here cannot change the result
@@ -263,7 +281,12 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   if (stamps) (void)hipFree(stamps);
   if (start) (void)hipEventDestroy(start);
   if (stop) (void)hipEventDestroy(stop);
-  drop_graphs();
+  if (sstart) (void)hipEventDestroy(sstart);
+  if (sstop) (void)hipEventDestroy(sstop);
+  for (int i = 0; i < 4; ++i) {
+    if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
+    if (graphs[i]) (void)hipGraphDestroy(graphs[i]);
+  }
   (void)hipStreamDestroy(s);
   return rc;
 }
@@ -311,6 +334,12 @@ int scratch_for_current_device(void **ptr) {
 }  // namespace
 
 void set_error(const std::string &message) { g_last_error = message; }
+
+namespace {
+constexpr int kDefaultSpinLimit = 1 << 20;
+std::atomic<int> g_spin_limit{kDefaultSpinLimit};
+}  // namespace
+int wait_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
 }  // namespace i8conv
 
@@ -556,17 +585,39 @@ int i8conv_launch_noalloc(int id, const i8conv_shape *shape, const int8_t *input
 // ---- requantized int8 output -------------------------------------------------
 
 namespace {
-// The dispatched plan when it is the row kernel with copy waves, whose
-// epilogue requantizes.
-bool fused_requant_plan(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *pp) {
-  return dispatch(s) == I8CONV_KERNEL_HALO && plan_halo(s, g, pp) && pp->row && pp->streamed;
+// Where the dispatched kernel for a shape requantizes: in its own epilogue
+// (the row kernel with copy waves; the pointwise streaming form with a
+// requantizing instance; split-K's second pass; the pipelined GEMM's
+// epilogue), or not at all (the convolution into an int32 workspace, then
+// a requantizing pass).
+enum RequantRoute { kRqUnfused, kRqRow, kRqPointwise, kRqSplitK, kRqGemm };
+
+RequantRoute requant_route(const i8conv_shape &s, const i8conv_geometry &g) {
+  const int id = dispatch(s);
+  PatchPlan pp;
+  if (id == I8CONV_KERNEL_HALO && plan_halo(s, g, &pp) && pp.row && pp.streamed) return kRqRow;
+  if (id == I8CONV_KERNEL_GENERIC && plan_generic(s, g).pw &&
+      pointwise_requant_supported(s.c, int(g.gemm_n)))
+    return kRqPointwise;
+  if (id == I8CONV_KERNEL_SPLITK && g.gemm_n % 4 == 0) return kRqSplitK;
+  if (id == I8CONV_KERNEL_GENERIC && g.gemm_n % 4 == 0 && plan_generic(s, g).dma) return kRqGemm;
+  return kRqUnfused;
 }
-// The dispatched plan when it is the generic kernel's pointwise streaming
-// form with a requantizing instance (used when bias, mult, shift and the
-// output are 16-byte aligned).
-bool pointwise_requant_plan(const i8conv_shape &s, const i8conv_geometry &g, int id) {
-  return id == I8CONV_KERNEL_GENERIC && plan_generic(s, g).pw &&
-         pointwise_requant_supported(s.c, int(g.gemm_n));
+
+// The pointer alignment a fused route's epilogue needs (16-byte vector
+// loads of bias, mult and shift; the pointwise form's 16-byte stores).
+// Without it the launch goes the unfused way.
+bool requant_route_aligned(RequantRoute r, const int32_t *bias, const int32_t *mult,
+                           const int32_t *shift, const int8_t *output) {
+  switch (r) {
+    case kRqRow: return true;  // the row kernel falls back to element stores itself
+    case kRqPointwise:
+      return aligned(bias, 16) && aligned(mult, 16) && aligned(shift, 16) && aligned(output, 16);
+    case kRqSplitK:
+      return aligned(bias, 16) && aligned(mult, 16) && aligned(shift, 16) && aligned(output, 4);
+    case kRqGemm: return aligned(mult, 16) && aligned(shift, 16) && aligned(output, 4);
+    default: return false;
+  }
 }
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 }  // namespace
@@ -593,17 +644,16 @@ int i8conv_requant_fused(const i8conv_shape *shape) {
   if (!shape) return 0;
   i8conv_geometry g;
   if (derive(*shape, &g) != I8CONV_OK) return 0;
-  PatchPlan pp;
-  return fused_requant_plan(*shape, g, &pp) || pointwise_requant_plan(*shape, g, dispatch(*shape))
-             ? 1
-             : 0;
+  return requant_route(*shape, g) != kRqUnfused ? 1 : 0;
 }
 
 size_t i8conv_requant_workspace_bytes(const i8conv_shape *shape) {
   if (!shape) return 0;
   i8conv_geometry g;
   if (derive(*shape, &g) != I8CONV_OK) return 0;
-  if (i8conv_requant_fused(shape)) return i8conv_dispatch_workspace_bytes(shape);
+  // fused: the dispatched kernel's own workspace (split-K's partial sums;
+  // nothing for the others)
+  if (requant_route(*shape, g) != kRqUnfused) return i8conv_dispatch_workspace_bytes(shape);
   return align256(size_t(g.output_elements) * 4) + i8conv_dispatch_workspace_bytes(shape);
 }
 
@@ -628,53 +678,52 @@ int i8conv_launch_requant(const i8conv_shape *shape, const int8_t *input, const 
     return I8CONV_BAD_ARGUMENT;
   }
   const int id = dispatch(*shape);
-  PatchPlan pp;
-  if (id == I8CONV_KERNEL_HALO && plan_halo(*shape, g, &pp) && pp.row && pp.streamed) {
-    // fused: the output is < 2 GiB (the plan checks it)
-    const ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
+  const RequantRoute route = requant_route(*shape, g);
+  if (route != kRqUnfused && requant_route_aligned(route, bias, mult, shift, output)) {
+    ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
     const RequantArgs q{mult, shift, zero_point, output};
-    return launch_rowpass(args, pp, stream, &q);
-  }
-  if (pointwise_requant_plan(*shape, g, id) && aligned(bias, 16) && aligned(mult, 16) &&
-      aligned(shift, 16) && aligned(output, 16)) {
-    // fused: the pointwise form's eligibility keeps the output < 2 GiB
-    const ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
-    const RequantArgs q{mult, shift, zero_point, output};
-    return launch_pointwise(args, &q, stream);
+    switch (route) {
+      case kRqRow: {
+        // the output is < 2 GiB (the plan checks it)
+        PatchPlan pp;
+        plan_halo(*shape, g, &pp);
+        return launch_rowpass(args, pp, stream, &q);
+      }
+      case kRqPointwise:
+        // the pointwise form's eligibility keeps the output < 2 GiB
+        return launch_pointwise(args, &q, stream);
+      case kRqSplitK: {
+        // split-K's second pass requantizes as it adds the splits: only the
+        // partial sums need the workspace
+        const size_t need = i8conv_workspace_bytes(I8CONV_KERNEL_SPLITK, shape);
+        if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) {
+          set_error("requantized split-K launch needs a 256-byte aligned workspace of " +
+                    std::to_string(need) + " bytes");
+          return I8CONV_WORKSPACE_TOO_SMALL;
+        }
+        return launch_splitk(args, plan_splitk(*shape, g), workspace, stream, &q);
+      }
+      default:
+        // the pipelined GEMM's epilogue requantizes: no workspace
+        args.q_mult = mult;
+        args.q_shift = shift;
+        args.q_zp = zero_point;
+        args.q_y = output;
+        return launch_gemm(args, plan_generic(*shape, g), stream);
+    }
   }
   const size_t acc_bytes = align256(size_t(g.output_elements) * 4);
   const size_t need = acc_bytes + i8conv_workspace_bytes(id, shape);
   if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) {
     set_error("requantized launch needs a 256-byte aligned workspace of " + std::to_string(need) +
               " bytes" +
-              (pointwise_requant_plan(*shape, g, id)
+              (route != kRqUnfused
                    ? std::string(" (or bias, mult, shift and output 16-byte aligned)")
                    : std::string()));
     return I8CONV_WORKSPACE_TOO_SMALL;
   }
   int32_t *acc = static_cast<int32_t *>(workspace);
   void *conv_ws = static_cast<char *>(workspace) + acc_bytes;
-  if (id == I8CONV_KERNEL_SPLITK && g.gemm_n % 4 == 0 && aligned(bias, 16) && aligned(mult, 16) &&
-      aligned(shift, 16) && aligned(output, 4)) {
-    // split-K's second pass requantizes as it adds the splits: the
-    // workspace's int32 output region goes unused
-    const ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
-    const RequantArgs q{mult, shift, zero_point, output};
-    return launch_splitk(args, plan_splitk(*shape, g), conv_ws, stream, &q);
-  }
-  if (id == I8CONV_KERNEL_GENERIC && g.gemm_n % 4 == 0 && aligned(mult, 16) &&
-      aligned(shift, 16) && aligned(output, 4)) {
-    const GemmPlan gp = plan_generic(*shape, g);
-    if (gp.dma) {
-      // the pipelined GEMM's epilogue requantizes: the workspace goes unused
-      ConvArgs args = make_args(*shape, g, input, filter, bias, nullptr);
-      args.q_mult = mult;
-      args.q_shift = shift;
-      args.q_zp = zero_point;
-      args.q_y = output;
-      return launch_gemm(args, gp, stream);
-    }
-  }
   const int r = i8conv_launch(id, shape, input, filter, bias, acc, conv_ws,
                               workspace_bytes - acc_bytes, stream);
   if (r != I8CONV_OK) return r;
@@ -815,6 +864,17 @@ int i8conv_stream_destroy(void *stream) {
   const hipError_t e = hipStreamDestroy(static_cast<hipStream_t>(stream));
   return e == hipSuccess ? I8CONV_OK : hip_fail("hipStreamDestroy", e);
 }
+
+int i8conv_set_wait_spin_limit(int polls) {
+  if (polls < 0) {
+    set_error("set_wait_spin_limit needs polls >= 0");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  g_spin_limit.store(polls, std::memory_order_relaxed);
+  return I8CONV_OK;
+}
+
+int i8conv_wait_spin_limit(void) { return wait_spin_limit(); }
 
 int i8conv_wait_expired(int *expired) {
   if (!expired) {

@@ -179,6 +179,10 @@ size_t rowpass_lds_bytes(int wp, int rows);
 // kernel_rowpass.hip: reads and clears the device word its waves set when a
 // bounded wait gives up (synchronizes the device); *expired = 1 if it was set.
 int rowpass_wait_expired(int *expired);
+// capi.hip: polls each bounded chunk wait of the row kernel with copy waves
+// and the deep-channel split-K makes before it gives up; read at launch
+// (i8conv_set_wait_spin_limit; 2^20 by default)
+int wait_spin_limit();
 int launch_deepk(const ConvArgs &a, const DeepPlan &p, void *workspace, void *stream);
 int deepk_wait_expired(int *expired);
 // kernel_probe.hip: a store-only kernel (16-byte buffer stores, write-through

@@ -63,7 +63,6 @@ namespace {
 
 constexpr int kDkUnits = kDeepUnits;          // 16-byte units per plane pixel
 constexpr int kDkFilterBytes = 9 * 2 * 2048;  // taps x fragments x 16 rows x 128 B
-constexpr int kDkSpinLimit = 1 << 20;         // polls of about 64 cycles each
 constexpr int kDkMaxLoads = kDeepMaxLoadsPerWave;  // plane loads per copy wave
 
 // The source word of every flag copy.
@@ -84,6 +83,7 @@ struct DeepArgs {
   int per_xcd;      // grid / 8 when grid % 8 == 0, else 0 (no XCD order)
   int flags_lds;    // LDS byte offset of the chunk flags
   int planes_lds;   // LDS byte offset of the planes
+  int spin_limit;   // polls of about 64 cycles each per bounded wait (wait_spin_limit())
   FastDiv3 div_hw, div_w, div_hpwp, div_wp, div_ohw, div_ow;
 };
 
@@ -96,8 +96,8 @@ __device__ __forceinline__ bool flags_set(v4i f) {
   return __builtin_amdgcn_readfirstlane(f[0] & f[1] & f[2] & f[3]) != 0;
 }
 
-__device__ __forceinline__ void flag_wait(uint32_t addr) {
-  for (int spin = 0; spin < kDkSpinLimit; ++spin) {
+__device__ __forceinline__ void flag_wait(uint32_t addr, int spin_limit) {
+  for (int spin = 0; spin < spin_limit; ++spin) {
     v4i v;
     asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
     if (flags_set(v)) return;
@@ -249,9 +249,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
                    "v"(1)
                    : "memory");
   }
-  flag_wait(halo_flags);
+  flag_wait(halo_flags, p.spin_limit);
   // the slice's filter into VGPRs
-  flag_wait(flags);
+  flag_wait(flags, p.spin_limit);
   v4i A[9][2][2];
 #pragma unroll
   for (int t = 0; t < 9; ++t)
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
     // fragment reads is in that image or an earlier one)
     const int last = min(16 * f + 15, p.gemm_m - 1);
     const int need = int(fast_div(uint32_t(last), p.div_ohw)) + 1;
-    flag_wait(flags + 16u * uint32_t(need));
+    flag_wait(flags + 16u * uint32_t(need), p.spin_limit);
     v4i acc[2][2];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -388,6 +388,7 @@ int launch_deepk(const ConvArgs &a, const DeepPlan &p, void *workspace, void *st
   h.x = a.x;
   h.w = a.w;
   h.partial = static_cast<int32_t *>(workspace);
+  h.spin_limit = wait_spin_limit();
   h.x_bytes = a.x_bytes;
   h.w_bytes = a.w_bytes;
   h.partial_bytes = uint32_t(int64_t(p.splits) * a.gemm_m * a.gemm_n * 4);

@@ -336,23 +336,25 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
   args.partial = static_cast<int32_t *>(workspace);
   args.splits = p.splits;
   args.stages_per_split = p.stages_per_split;
-  int rc = p.deep  ? launch_deepk(args, p.deep_plan, workspace, stream)
-           : p.dma ? launch_gemm_dma(args, p, p.splits, stream)
-                   : launch_any(args, p, p.splits, s);
-  if (rc != I8CONV_OK) return rc;
   const size_t total = size_t(a.gemm_m) * size_t(a.gemm_n);
   const bool vec = (a.gemm_n & 3) == 0 &&
                    (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(a.bias) & 15) == 0;
-  const size_t work = vec ? total / 4 : total;
-  size_t blocks = (work + kThreads - 1) / kThreads;
-  if (blocks > 4096) blocks = 4096;
-  if (blocks == 0) blocks = 1;
+  // rejected before the first pass is enqueued, so that an error leaves
+  // nothing queued
   if (rq && !vec) {
     set_error("split-K requantized reduce needs N % 4 == 0 and 16-byte aligned bias and workspace");
     return I8CONV_BAD_ARGUMENT;
   }
+  int rc = p.deep  ? launch_deepk(args, p.deep_plan, workspace, stream)
+           : p.dma ? launch_gemm_dma(args, p, p.splits, stream)
+                   : launch_any(args, p, p.splits, s);
+  if (rc != I8CONV_OK) return rc;
+  const size_t work = vec ? total / 4 : total;
+  size_t blocks = (work + kThreads - 1) / kThreads;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks == 0) blocks = 1;
   if (rq) {
     hipLaunchKernelGGL(splitk_reduce_vec<true>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
                        args.partial, a.bias, nullptr, a.gemm_n / 4, total / 4, p.splits, rq->mult,

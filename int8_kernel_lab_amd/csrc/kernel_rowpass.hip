@@ -96,21 +96,22 @@ struct PassArgs {
   int plane_copies;  // 1 KB copies per plane: ceil(wp * kUnits / 64)
   int rows_in;       // input rows per block: R + 2
   int blocks, tiles_n;
+  int spin_limit;    // polls of a bounded chunk wait (wait_spin_limit())
   FastDiv3 div_plane_copies, div_hp, div_blocks, div_tiles_n;
 };
 
 // Cross-wave signals in LDS: flag words set by LDS-DMA flag copies behind
 // each chunk (see the top of this file), polled by the MFMA waves.
-// The wait is bounded: after kSpinLimit polls (each a read and a sleep of
-// about 64 cycles, some tens of ms in all, far beyond any real copy time) it
-// gives up, so that every wave always reaches the end of the kernel.  A
+// The wait is bounded: after spin_limit polls (each a read and a sleep of
+// about 64 cycles; by default 2^20, some tens of ms in all, far beyond any
+// real copy time) it gives up, so that every wave always reaches the end of
+// the kernel.  The host lowers the limit only to test the give-up path
+// (i8conv_set_wait_spin_limit: 0 gives up at the first wait).  A
 // wave that gives up goes on with LDS contents that may not have landed,
 // so it records the give-up in g_wait_expired (a vector store to global
 // memory); the host reads and clears that word with i8conv_wait_expired()
 // after synchronizing, and must treat the output of the launches since the
 // last check as wrong when it is set.
-constexpr int kSpinLimit = 1 << 20;
-
 // The source word of every flag copy.
 __device__ __attribute__((aligned(16))) int g_flag_one[4] = {1, 1, 1, 1};
 
@@ -126,8 +127,8 @@ __device__ __forceinline__ bool flags_set(v4i f) {
   return __builtin_amdgcn_readfirstlane(f[0] & f[1] & f[2] & f[3]) != 0;
 }
 
-__device__ __forceinline__ void flag_wait(uint32_t addr) {
-  for (int spin = 0; spin < kSpinLimit; ++spin) {
+__device__ __forceinline__ void flag_wait(uint32_t addr, int spin_limit) {
+  for (int spin = 0; spin < spin_limit; ++spin) {
     v4i v;
     asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
     if (flags_set(v)) return;
@@ -254,7 +255,7 @@ struct PassState {
     if (IR + 1 < OHI + 2) {
       const v4i seen = peeked;
       if (IR + 2 < OHI + 2) peeked = flag_peek(counter<G>(p, IR + 2));
-      if (!flags_set(seen)) flag_wait(counter<G>(p, IR + 1));
+      if (!flags_set(seen)) flag_wait(counter<G>(p, IR + 1), p.spin_limit);
       // keeps the compiler from moving the plain LDS reads of load_row (and
       // take_taps) above the flag test on the path that skips flag_wait
       // (whose asm already orders them); the hardware issues a wave's LDS
@@ -355,7 +356,7 @@ struct PassState {
   template <int G, int kMode, size_t... I>
   __device__ __forceinline__ void walk(const PassArgs &p, int rows_out, int m_row0, int oc0,
                                        int lane, std::index_sequence<I...>) {
-    flag_wait(counter<G>(p, OLO));
+    flag_wait(counter<G>(p, OLO), p.spin_limit);
     peeked = flag_peek(counter<G>(p, OLO + 1));
     take_taps<G, 0>(lane);
     load_row<G>(p, OLO);
@@ -702,6 +703,7 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream, const Re
   h.rows_in = R + 2;
   h.blocks = p.ranges;
   h.tiles_n = p.tiles_n;
+  h.spin_limit = wait_spin_limit();
   h.div_plane_copies = make_fastdiv3(uint32_t(h.plane_copies));
   h.div_hp = make_fastdiv3(uint32_t(h.hp));
   h.div_blocks = make_fastdiv3(uint32_t(h.blocks));

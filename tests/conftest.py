@@ -50,12 +50,13 @@ def baseline_cases():
 
 @pytest.fixture(autouse=True)
 def _no_expired_waits(request):
-    """After every GPU test: no bounded wait of the row kernel with copy
-    waves gave up (i8conv_wait_expired), so no launch of the test returned
-    I8CONV_OK over an output computed from data that had not landed."""
+    """After every GPU test: no bounded wait (row kernel with copy waves or
+    deep-channel split-K) gave up (i8conv_wait_expired), so no launch of the
+    test returned I8CONV_OK over an output computed from data that had not
+    landed."""
     yield
     if request.node.get_closest_marker("gpu") is None:
         return
     import int8_kernel_lab_amd as lab
     assert not lab.wait_expired(), \
-        f"{request.node.nodeid}: a row-kernel wait gave up; its outputs are not to be trusted"
+        f"{request.node.nodeid}: a bounded wait gave up; its outputs are not to be trusted"

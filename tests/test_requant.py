@@ -108,17 +108,23 @@ def _baseline(name):
     return lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), name)
 
 
-def test_requant_fused_for_the_row_kernel_with_copy_waves_and_the_pointwise_form():
+def test_requant_fused_where_the_dispatched_kernel_requantizes():
     assert lab.requant_fused(_baseline("cfg2_resnet_3x3_s1"))
     # the generic kernel's pointwise streaming form, slices of 64 channels
     assert lab.requant_fused(_baseline("cfg4a_pointwise_1x1"))
     assert lab.requant_workspace_bytes(_baseline("cfg4a_pointwise_1x1")) == 0
-    for name in ("cfg1_smoke", "cfg3_down_3x3_s2", "cfg5a_deep_k"):
-        assert not lab.requant_fused(_baseline(name))
-    # pointwise slices of 32 channels (C = 512) or 256 (C = 64, N = 256)
-    # have no requantizing instance
-    for shape in (lab.ConvShape(1, 8, 8, 512, 64, 1, 1, 0, 0, 1, 1, 1, 1),
-                  lab.ConvShape(1, 8, 8, 64, 256, 1, 1, 0, 0, 1, 1, 1, 1),
+    # the pipelined GEMM's epilogue and split-K's second pass
+    for name in ("cfg3_down_3x3_s2", "cfg5b_dilated", "cfg5a_deep_k"):
+        assert lab.requant_fused(_baseline(name)), name
+    # the row kernel without copy waves (C = 64) has no requantizing epilogue
+    assert not lab.requant_fused(_baseline("cfg1_smoke"))
+    # pointwise slices of 32 channels (C = 512) have no requantizing
+    # instance: the pipelined GEMM (C % 128 == 0) requantizes in its
+    # epilogue instead; slices of 256 (C = 64, N = 256) or 32 channels with
+    # C = 64 go unfused (the register-staged GEMM has no such epilogue)
+    wide = lab.ConvShape(1, 8, 8, 512, 64, 1, 1, 0, 0, 1, 1, 1, 1)
+    assert lab.requant_fused(wide) and lab.requant_workspace_bytes(wide) == 0
+    for shape in (lab.ConvShape(1, 8, 8, 64, 256, 1, 1, 0, 0, 1, 1, 1, 1),
                   lab.ConvShape(1, 8, 8, 64, 32, 1, 1, 0, 0, 1, 1, 1, 1)):
         assert not lab.requant_fused(shape), shape
 
@@ -126,18 +132,35 @@ def test_requant_fused_for_the_row_kernel_with_copy_waves_and_the_pointwise_form
 def test_requant_workspace_sizes():
     s2 = _baseline("cfg2_resnet_3x3_s1")
     assert lab.requant_workspace_bytes(s2) == 0
+    # the pipelined GEMM's epilogue writes no int32 tensor: no workspace
     s3 = _baseline("cfg3_down_3x3_s2")
-    assert lab.requant_workspace_bytes(s3) == s3.output_elements * 4  # already 256-aligned
+    assert lab.requant_workspace_bytes(s3) == 0
+    # split-K's second pass requantizes: only the partial sums
     s5 = _baseline("cfg5a_deep_k")
-    acc = (s5.output_elements * 4 + 255) // 256 * 256
-    assert lab.requant_workspace_bytes(s5) == acc + lab.workspace_bytes("splitk", s5)
+    assert lab.requant_workspace_bytes(s5) == lab.workspace_bytes("splitk", s5)
+    # unfused (the C = 64 row kernel): the int32 output, 256-byte aligned
+    s1 = _baseline("cfg1_smoke")
+    acc = (s1.output_elements * 4 + 255) // 256 * 256
+    assert lab.requant_workspace_bytes(s1) == acc + lab.workspace_bytes(lab.dispatch(s1), s1)
 
 
 def test_requant_launch_errors_without_gpu():
     s3 = _baseline("cfg3_down_3x3_s2")
     fake = 1 << 20  # never dereferenced: the checks fail before any launch
+    # unfused (the C = 64 row kernel) without a workspace
     with pytest.raises(lab.I8ConvError) as e:
-        lab.launch_requant(s3, fake, fake, fake, fake, fake, 0, fake, None, 0)
+        lab.launch_requant(_baseline("cfg1_smoke"), fake, fake, fake, fake, fake, 0, fake, None, 0)
+    assert e.value.status == _lib.WORKSPACE_TOO_SMALL
+    # the pipelined GEMM fuses only with 16-byte aligned mult and shift: a
+    # multiplier array at +4 bytes takes the unfused way, which needs the
+    # int32 workspace
+    with pytest.raises(lab.I8ConvError, match="16-byte aligned") as e:
+        lab.launch_requant(s3, fake, fake, fake, fake + 4, fake, 0, fake, None, 0)
+    assert e.value.status == _lib.WORKSPACE_TOO_SMALL
+    # fused split-K still needs its partial sums' workspace
+    with pytest.raises(lab.I8ConvError, match="split-K") as e:
+        lab.launch_requant(_baseline("cfg5a_deep_k"), fake, fake, fake, fake, fake, 0, fake,
+                           None, 0)
     assert e.value.status == _lib.WORKSPACE_TOO_SMALL
     with pytest.raises(lab.I8ConvError) as e:
         lab.launch_requant(s3, fake, fake, fake, None, fake, 0, fake, fake, 1 << 30)
