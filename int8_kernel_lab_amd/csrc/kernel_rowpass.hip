@@ -158,6 +158,7 @@ struct PassState {
   int plane_bytes;
   uint32_t flags;          // LDS address of the chunk flags: 16 bytes per chunk
   v4i peeked;              // flags of the next row's chunk, read one row ahead
+  v4i lastpeek;            // flags of the walk's last chunk (read at step OLO + kDecide - 1)
   // Output, vector path: a buffer resource over y, this lane's byte offset
   // of output row 0 per fragment (out of range where the column or the
   // channels fall outside the layer: the store is dropped, no branch), and
@@ -171,6 +172,10 @@ struct PassState {
   v4i qm, qs;
   v4i qam, qhh, qsh;
   bool qshort;
+
+  // steps of a walk that test each row's chunk flags before the walk tests
+  // its last chunk's
+  static constexpr int kDecide = 4;
 
   static constexpr int mfmas_in_step(int ir) {
     int n = 0;
@@ -233,7 +238,7 @@ struct PassState {
   // (compile-time valid ones); in the last walk, output row IR - 3 is then
   // stored.  The flags of the chunk after next are read here and tested
   // one row later, so a chunk that has landed costs no wait.
-  template <int G, int IR, int kMode>
+  template <int G, int IR, int kMode, bool kTest>
   __device__ __forceinline__ void step(const PassArgs &p, int rows_out, int m_row0, int oc0,
                                        int lane) {
     // Output row IR - 3 was completed by the previous row's MFMAs.
@@ -253,14 +258,19 @@ struct PassState {
 #pragma unroll
         for (int j = 0; j < NFR; ++j) cur[g][fx][j] = frag[g][fx][j];
     if (IR + 1 < OHI + 2) {
-      const v4i seen = peeked;
-      if (IR + 2 < OHI + 2) peeked = flag_peek(counter<G>(p, IR + 2));
-      if (!flags_set(seen)) flag_wait(counter<G>(p, IR + 1), p.spin_limit);
-      // keeps the compiler from moving the plain LDS reads of load_row (and
-      // take_taps) above the flag test on the path that skips flag_wait
-      // (whose asm already orders them); the hardware issues a wave's LDS
-      // operations in order, so no wait instruction is needed
-      asm volatile("" ::: "memory");
+      if constexpr (kTest) {
+        const v4i seen = peeked;
+        if (IR + 2 < OHI + 2) peeked = flag_peek(counter<G>(p, IR + 2));
+        // the last chunk's flags, tested before the steps that may skip
+        // their flag tests (walk)
+        if (IR + 1 == OLO + kDecide) lastpeek = flag_peek(counter<G>(p, OHI + 1));
+        if (!flags_set(seen)) flag_wait(counter<G>(p, IR + 1), p.spin_limit);
+        // keeps the compiler from moving the plain LDS reads of load_row
+        // (and take_taps) above the flag test on the path that skips
+        // flag_wait (whose asm already orders them); the hardware issues a
+        // wave's LDS operations in order, so no wait instruction is needed
+        asm volatile("" ::: "memory");
+      }
       constexpr int fy_next = IR + 1 - OLO;
       if (fy_next <= 2) take_taps<G, (fy_next <= 2 ? fy_next : 0)>(lane);
       load_row<G>(p, IR + 1);
@@ -352,10 +362,27 @@ struct PassState {
     }
   }
 
-  // The walk from group G over padded input rows OLO .. OHI + 1.
-  template <int G, int kMode, size_t... I>
+  // Steps OLO + From + I of the walk from group G, with or without the
+  // next row's flag test.
+  template <int G, int kMode, bool kTest, int From, size_t... I>
+  __device__ __forceinline__ void steps(const PassArgs &p, int rows_out, int m_row0, int oc0,
+                                        int lane, std::index_sequence<I...>) {
+    (step<G, OLO + From + int(I), kMode, kTest>(p, rows_out, m_row0, oc0, lane), ...);
+  }
+
+  // The walk from group G over padded input rows OLO .. OHI + 1.  The first
+  // kDecide steps test each next row's chunk flags; by then the copy waves
+  // have usually landed every chunk (they issue all copies without
+  // waiting), so the walk tests the flags of its last chunk once: if they
+  // are set, every chunk of the walk has landed (each copy wave's loads
+  // land in the order it issued them, its flag copy of a chunk after the
+  // chunk's copies), and the remaining steps run without flag tests, whose
+  // read-test-branch sequence left the MFMA pipe idle for some cycles per
+  // row (28x28x128: ~20 ns per row step).
+  template <int G, int kMode>
   __device__ __forceinline__ void walk(const PassArgs &p, int rows_out, int m_row0, int oc0,
-                                       int lane, std::index_sequence<I...>) {
+                                       int lane) {
+    constexpr int kSteps = OHI - OLO + 2;
     flag_wait(counter<G>(p, OLO), p.spin_limit);
     peeked = flag_peek(counter<G>(p, OLO + 1));
     take_taps<G, 0>(lane);
@@ -368,12 +395,26 @@ struct PassState {
 #pragma unroll
         for (int j = 0; j < NFR; ++j) acc[r][j] = bv;
     }
-    (step<G, OLO + int(I), kMode>(p, rows_out, m_row0, oc0, lane), ...);
+    if constexpr (kDecide + 1 < kSteps) {
+      steps<G, kMode, true, 0>(p, rows_out, m_row0, oc0, lane,
+                               std::make_index_sequence<kDecide>{});
+      if (flags_set(lastpeek))
+        steps<G, kMode, false, kDecide>(p, rows_out, m_row0, oc0, lane,
+                                        std::make_index_sequence<kSteps - kDecide>{});
+      else
+        steps<G, kMode, true, kDecide>(p, rows_out, m_row0, oc0, lane,
+                                       std::make_index_sequence<kSteps - kDecide>{});
+    } else {
+      steps<G, kMode, true, 0>(p, rows_out, m_row0, oc0, lane,
+                               std::make_index_sequence<kSteps>{});
+    }
   }
 };
 
-// Eight waves: waves 0-3 run the MFMAs (16 output channels each), waves 4-7
-// only copy.  The copies are issued in chunks, in the order the MFMA waves
+// Eight waves: waves 0-3 only copy, waves 4-7 run the MFMAs (16 output
+// channels each; wave w and MFMA wave w + 4 share a SIMD).  The copy waves
+// come first so that they are launched first and start issuing a little
+// earlier.  The copies are issued in chunks, in the order the MFMA waves
 // consume them: padded input row r (of the walk's groups), preceded for
 // r <= 2 by the filter taps of filter row r (the first row an input row
 // needs them at: input row r feeds output rows r - fy), and the bias first
@@ -473,11 +514,8 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
   // the element-store code (28x28x128: 5.52 -> 5.41 us per launch).
   auto walks = [&](auto mode) {
     constexpr int M = decltype(mode)::value;
-    st.template walk<0, M>(p, rows_out, m_row0, oc0, lane,
-                           std::make_index_sequence<OHI - OLO + 2>{});
-    if constexpr (NG == 1)
-      st.template walk<1, M>(p, rows_out, m_row0, oc0, lane,
-                             std::make_index_sequence<OHI - OLO + 2>{});
+    st.template walk<0, M>(p, rows_out, m_row0, oc0, lane);
+    if constexpr (NG == 1) st.template walk<1, M>(p, rows_out, m_row0, oc0, lane);
     st.template store_row<OHI - 1>(p, M != kStoreElem, rows_out, m_row0, oc0, lane);
   };
   if (vec && !kQ && rows_out >= OHI)
@@ -509,8 +547,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool copier = wave_id >= 4;
-  // the MFMA wave this wave is (or copies the filter halves and bias for)
+  const bool copier = wave_id < 4;
+  // the MFMA wave this wave is, 0..3 (or copies the filter halves and bias for)
   const int wave = wave_id & 3;
 
   const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
