@@ -6,24 +6,24 @@ the layer the >=50%-of-peak target is quoted on), on one GPU.
 A step = one convolution of the whole layer (7.40 GOP) with input, filter,
 bias and output resident in HBM.  Before timing, the GPU output is checked
 bit-exact against the CPU oracle (the reference's check-before-time
-contract, conv_lab.cu:193-194).  Timing (i8conv_measure_graph): the K steps
-are K back-to-back launches captured in one HIP graph (K <= 10000; larger
-K: graphs of 10000 and a remainder), replayed after a warmup of at least W
-launches AND at least --min-warmup-ms of wall time (back-to-back launches
-need some tens of ms to bring the clocks to their steady state) that ends
-in ~5 ms of replays the host does not wait for: the timed replays are
-enqueued behind them, so the GPU does not idle between the warmup and the
-timed launches (an idle of some hundred microseconds there let the first
-launches after it run ~10 % slower).  The time is taken between two HIP
-events recorded on the graph's stream.  A graph replay begins some
-microseconds after the previous one ends; the timed region holds that gap
-once per replay, so it weighs on short runs (28x28x128: about 0.4 us per
-launch at K = 20, 0.004 us at K = 2000); config.stamped_ms_per_step leaves
-it out (the same launches from graphs that begin and end with a device
-clock-stamp kernel, replayed right before the event-timed ones).
-The output is poisoned before those replays and checked against the
-oracle after them.  Beside it: the same K launches enqueued one by one
-on a stream, and the reference's per-launch median (conv_lab.cu:88-110).
+contract, conv_lab.cu:193-194).  Timing (i8conv_measure_graph): a warmup
+of at least W launches AND at least --min-warmup-ms of wall time (back-to-
+back launches need some tens of ms to bring the clocks to their steady
+state), replayed from a HIP graph, ends in ~5 ms of replays the host does
+not wait for; the timed launches are enqueued behind them, so the GPU does
+not idle between the warmup and the timed launches.  The headline
+(ms_per_step) is the K steps as K back-to-back launches enqueued one by one
+on the stream between two HIP events (stream region), like the reference's
+launches (conv_lab.cu:88-110) but batched; the output is poisoned right
+before them and checked against the oracle after them.  Beside it, the same
+K launches as replays of a HIP graph of K launches (K <= 10000; larger K:
+graphs of 10000 and a remainder) between events (config.graph_ms_per_step):
+each graph replay begins some microseconds after the previous one ends, a
+gap the graph region holds once per replay, which weighs on short runs
+(28x28x128: about 0.4 us per launch at K = 20, 0.004 us at K = 2000); and
+the same graphs between device clock stamps captured inside them
+(config.stamped_ms_per_step, without that gap).  Also the reference's
+per-launch median (conv_lab.cu:88-110).
 The CPU baseline is the C oracle (a port of conv_lab.cu:39-66) timed on
 this host, single-threaded and on all threads of the box's CPU share.
 
@@ -135,8 +135,10 @@ def write_floor(workload: str, steps: int, warmup: int, min_warmup_ms: float) ->
     store-only kernel (i8conv_measure_store_floor) writing exactly the
     layer's int32 output bytes with the row kernel's 16-byte write-through
     stores, in its launch shape (workgroups x 512 threads, the same dynamic
-    LDS), timed like the headline; beside it, an empty kernel of the same
-    shape (the dispatch floor) and ordinary stores."""
+    LDS), timed as graph replays between events (the headline's
+    graph_ms_per_step method: a short kernel's stream launches can be
+    host-bound); beside it, an empty kernel of the same shape (the dispatch
+    floor) and ordinary stores."""
     import numpy as np
     import int8_kernel_lab_amd as lab
     shape = lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), workload)
@@ -326,22 +328,23 @@ def main() -> int:
               file=sys.stderr)
         return 1
 
-    # the timed steps: graph replays; the output is poisoned right before
-    # them, so the check afterwards covers exactly the timed launches
+    # the timed steps (stream region, the headline; graph and stamped
+    # figures beside it); the output is poisoned right before the stream
+    # region, so the check afterwards covers exactly the timed launches
     per_graph = min(args.steps, 10000)
     t = lab.measure_graph(kernel, shape, xb, wb, bb, yb, ws, ws_n, warmup=args.warmup,
                           min_warmup_ms=args.min_warmup_ms, iterations=args.steps,
                           launches_per_graph=per_graph, poison_byte=0xA5)
-    mean_ms = t["mean_ms"]
+    mean_ms = t["stream_ms"]
     got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
     if not np.array_equal(got, expected):
         print(f"bench.py: {kernel} output after the timed replays differs from the oracle",
               file=sys.stderr)
         return 1
-    # beside it, right after (the clocks are warm): the same launches on a
-    # stream one by one, and the reference's per-launch median
-    median_ms, stream_ms = lab.measure(kernel, shape, xb, wb, bb, yb, ws, ws_n,
-                                       warmup=args.warmup, iterations=args.steps)
+    # beside it, right after (the clocks are warm): the reference's
+    # per-launch median (each launch between its own events, synchronized)
+    median_ms, _ = lab.measure(kernel, shape, xb, wb, bb, yb, ws, ws_n,
+                               warmup=args.warmup, iterations=args.steps)
     if lab.wait_expired():
         print(f"bench.py: a bounded wait of {kernel} gave up during the timed launches",
               file=sys.stderr)
@@ -352,8 +355,7 @@ def main() -> int:
     gbps = nbytes / (mean_ms * 1e-3) / 1e9
     info = lab.device_info()
     cpu = None if args.no_cpu_baseline else cpu_baseline(shape, x, w, b)
-    graphs = (f"{t['full_replays']} replay(s) of a HIP graph of {t['launches_per_graph']} "
-              f"launches between events recorded on its stream")
+    graphs = f"{t['full_replays']} replay(s) of a HIP graph of {t['launches_per_graph']} launches"
     if t["remainder_launches"]:
         graphs += f" + a graph of {t['remainder_launches']}"
 
@@ -379,20 +381,20 @@ def main() -> int:
             "ops_per_step": ops,
             "algorithmic_bytes_per_step": nbytes,
             "pct_int8_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
-            "timing": f"{args.steps} back-to-back launches timed as {graphs}, after "
-                      f"{t['warmup_launches']} warmup launches over {t['warmup_ms']:.0f} ms, the "
-                      f"last ~5 ms of them enqueued with the timed replays behind them (no idle "
-                      f"GPU between warmup and timing); output poisoned before and checked "
-                      f"after the replays",
+            "timing": f"{args.steps} back-to-back launches enqueued one by one on a stream "
+                      f"between two events, after {t['warmup_launches']} warmup launches over "
+                      f"{t['warmup_ms']:.0f} ms whose last ~5 ms the host does not wait for (the "
+                      f"timed launches are enqueued behind them: no idle GPU between warmup and "
+                      f"timing); output poisoned before and checked after the timed launches",
             "warmup_launches_run": t["warmup_launches"],
             "warmup_ms": round(t["warmup_ms"], 1),
-            # the same K launches from graphs that begin and end with a
-            # clock-stamp kernel: device clock from the first launch's
-            # start to the last one's end, without the gap before the first
-            # replay runs (the kernel's back-to-back rate at any K)
+            # the same K launches as graph replays, between events
+            # (holds one graph-start gap per replay)
+            "graph_ms_per_step": round(t["mean_ms"], 6),
+            "graph_timing": graphs,
+            # the same graphs between device clock stamps captured inside
+            # them: the launches plus one stamp dispatch, without that gap
             "stamped_ms_per_step": round(t["stamped_ms"], 6),
-            "stream_behind_warm_ms_per_step": round(t["stream_ms"], 6),
-            "stream_ms_per_step": round(stream_ms, 6),
             "per_launch_median_ms": round(median_ms, 6),
             "device": info["arch"],
             "compute_units": info["compute_units"],

@@ -268,7 +268,7 @@ int i8conv_device_info(int *compute_units, int *clock_khz, char *arch_name,
 
 /* Result of i8conv_measure_graph. */
 typedef struct i8conv_graph_timing {
-  float mean_ms;          /* timed elapsed / iterations */
+  float mean_ms;          /* graph region: elapsed / iterations */
   int launches_per_graph; /* launches in the main graph */
   int full_replays;       /* replays of the main graph in the timed region */
   int remainder_launches; /* launches of the remainder graph (0: none) */
@@ -281,8 +281,8 @@ typedef struct i8conv_graph_timing {
    * starts running */
   float stamped_ms;
   /* the same K launches enqueued one by one on the stream (no graph),
-   * between one pair of events, right after the stamped region: elapsed /
-   * iterations */
+   * between one pair of events, after the poison fill that follows the
+   * graph region: elapsed / iterations */
   float stream_ms;
 } i8conv_graph_timing;
 
@@ -305,19 +305,18 @@ typedef struct i8conv_graph_timing {
  *      runs from the first graph's start stamp to the last one's end stamp
  *      (the launches plus one stamp dispatch, without the gap before each
  *      graph replay begins to run);
- *   5b. stream region: the K launches enqueued one by one on the stream
- *      (not from a graph) between one pair of events (stream_ms); they are
- *      enqueued while the tail still runs, so the GPU does not wait for
- *      the host;
- *   6. when poison_byte >= 0, the output is filled with that byte (a fill
- *      on the stream, outside any graph), so that it then holds only what
- *      the event-timed replays wrote;
- *   7. event-timed region: iterations / L main-graph replays plus the
+ *   6. event-timed graph region: iterations / L main-graph replays plus the
  *      remainder graph, exactly `iterations` launches, between one pair of
  *      events recorded on the stream (mean_ms).  Each graph replay begins
  *      with a gap of some microseconds after the previous one, which the
  *      region holds once per replay: a larger L spreads it over more
- *      launches.
+ *      launches;
+ *   7. when poison_byte >= 0, the output is filled with that byte (a fill on
+ *      the stream, outside any graph); then the stream region: the K
+ *      launches enqueued one by one on the stream (no graph) between one
+ *      pair of events (stream_ms).  They are enqueued while the tail still
+ *      runs, so the GPU does not wait for the host, and the output then
+ *      holds only what they wrote.
  * Fills *timing.  Synchronous. */
 int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
                          const int8_t *filter, const int32_t *bias, int32_t *output,

@@ -132,8 +132,8 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   hipGraphExec_t execs[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t start = nullptr, stop = nullptr, sstart = nullptr, sstop = nullptr;
   // fills the output with the poison byte, enqueued on the stream (a fill
-  // kernel outside any graph), so that a check after the event-timed
-  // replays sees only what they wrote
+  // kernel outside any graph), so that a check after the stream region
+  // sees only what its launches wrote
   auto poison = [&]() {
     if (poison_byte < 0 || out_bytes == 0) return int(I8CONV_OK);
     const hipError_t pe = hipMemsetAsync(output, poison_byte, out_bytes, s);
@@ -237,18 +237,19 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   if (rc == I8CONV_OK && (e = hipMemsetAsync(stamps, 0, stamp_bytes, s)) != hipSuccess)
     rc = hip_fail("hipMemsetAsync(stamps)", e);
   if (rc == I8CONV_OK) rc = replay_all(2);
-  // stream region: the K launches enqueued one by one on the stream, not
-  // from a graph, between one pair of events (enqueued while the tail
-  // still runs, so the GPU does not wait for the host)
-  if (rc == I8CONV_OK && (e = hipEventRecord(sstart, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-  for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch(s);
-  if (rc == I8CONV_OK && (e = hipEventRecord(sstop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-  // event-timed region: the output poisoned, then exactly `iterations`
-  // launches between one pair of events
-  if (rc == I8CONV_OK) rc = poison();
+  // event-timed graph region: exactly `iterations` launches from the main
+  // and remainder graphs between one pair of events
   if (rc == I8CONV_OK && (e = hipEventRecord(start, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
   if (rc == I8CONV_OK) rc = replay_all(0);
   if (rc == I8CONV_OK && (e = hipEventRecord(stop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  // stream region: the output poisoned, then the K launches enqueued one by
+  // one on the stream (no graph) between one pair of events; they are
+  // enqueued while the tail still runs, so the GPU does not wait for the
+  // host, and the output then holds only what they wrote
+  if (rc == I8CONV_OK) rc = poison();
+  if (rc == I8CONV_OK && (e = hipEventRecord(sstart, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
+  for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch(s);
+  if (rc == I8CONV_OK && (e = hipEventRecord(sstop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
   if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("hipStreamSynchronize", e);
   float ms = 0.f, sms = 0.f;
   if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess)
