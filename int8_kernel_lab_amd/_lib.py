@@ -2,7 +2,9 @@
 
 The library is built in-tree by ``__graft_entry__.build()`` (or ``make -C
 int8_kernel_lab_amd/csrc``).  There is no fallback: if it is missing, every
-entry point raises.
+entry point raises.  The environment variable I8CONV_LIBRARY names another
+build of the same ABI to load instead (the timeline tool's clock-stamped
+build, int8_kernel_lab_amd/timeline); unset, the in-tree library is loaded.
 """
 from __future__ import annotations
 
@@ -12,7 +14,7 @@ from ctypes import (POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int6
                     c_uint32, c_uint64, c_void_p)
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libi8conv.so")
+LIB_PATH = os.environ.get("I8CONV_LIBRARY") or os.path.join(HERE, "libi8conv.so")
 
 # Status codes (enum i8conv_status).
 OK = 0
