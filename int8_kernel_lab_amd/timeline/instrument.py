@@ -24,7 +24,7 @@ WAVES = 16   # wave slots per workgroup in the stamp buffer
 SLOTS = 32   # stamp slots per wave
 
 # Row kernel with copy waves: slot -> meaning
-ROWPASS_SLOTS = {0: "wave start", 1: "arguments loaded", 31: "after the flag barrier",
+ROWPASS_SLOTS = {0: "wave start", 1: "arguments loaded", 31: "past the flag barrier",
                  2: "copy wave: all copies issued", 3: "copy wave: copies landed",
                  27: "MFMA wave: walk start", 29: "MFMA wave: walk end",
                  30: "MFMA wave: stores drained"}
@@ -66,13 +66,14 @@ ROWPASS_EDITS = [
     ("  const PassArgs p = p_arg;\n  pin_sgprs(p);\n",
      "  const unsigned long long t_start = tl_now();\n  const PassArgs p = p_arg;\n  pin_sgprs(p);\n"
      "  tl_put(p.tl, 0, t_start);\n  tl_put(p.tl, 1, tl_now());\n"),
-    ("  __syncthreads();\n\n  if (copier) {",
-     "  __syncthreads();\n  tl_put(p.tl, 31, tl_now());\n\n  if (copier) {"),
+    ("  flag_barrier();\n  run_walk<",
+     "  flag_barrier();\n  tl_put(p.tl, 31, tl_now());\n  run_walk<"),
     ("    auto signal = [&](int c) {\n"
      "      if (lane == 0) lds_copy4(one, flags + 16u * uint32_t(c) + 4u * uint32_t(wave), 0u);\n"
      "    };",
      "    auto signal = [&](int c) {\n"
      "      if (lane == 0) lds_copy4(one, flags + 16u * uint32_t(c) + 4u * uint32_t(wave), 0u);\n"
+     "      if (c == 0) tl_put(p.tl, 31, tl_now());\n"
      "      if (c == nchunks - 1) tl_put(p.tl, 2, tl_now());\n"
      "    };"),
     ("    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n    // With a split",
