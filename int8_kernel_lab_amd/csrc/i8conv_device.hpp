@@ -142,6 +142,55 @@ I8_HD inline int32_t requant1_short(int32_t acc, uint32_t am, int32_t mult, uint
   return v < -128 ? -128 : (v > 127 ? 127 : v);
 }
 
+// Odd-multiplier form of requant1: one signed high multiply, one add, one
+// arithmetic shift and the clamp per value.  Write mult = mo * 2^t with mo
+// odd (t = trailing zeros) and s' = min(shift, 62) - t:
+// acc * mult / 2^s = acc * mo / 2^s'.  (mult = 0 takes mo = 0 and sh = 1:
+// (0 + k) >> 1 = zp.)  For
+// s' = 32 + sh with 1 <= sh <= 30, p = acc * mo and hi = floor(p / 2^32):
+//   p >= 0:            round(p / 2^s') = floor((hi + hh) / 2^sh)
+//                      (2^(s'-1) = hh * 2^32 with hh = 2^(sh-1) adds nothing
+//                      to the low word);
+//   p < 0, p not a multiple of 2^32:
+//                      hi = -floor(|p| / 2^32) - 1, and
+//                      -floor((-hi - 1 + hh) / 2^sh) = floor((hi + hh) / 2^sh)
+//                      (since -floor(x / d) = floor((-x + d - 1) / d) and
+//                      2^sh - hh = hh).
+// The one case left out, p < 0 a multiple of 2^32, needs acc * mo = 0 mod 2^32,
+// so acc = 0 (mo is odd, hence invertible mod 2^32), and then p = 0: it
+// never occurs.  So round(acc * mult / 2^s) = (hi + hh) >> sh exactly, and
+// with k = hh + zp * 2^sh (adding a multiple of 2^sh commutes with the
+// shift) zp + round(...) = (hi + k) >> sh.  |hi| <= 2^30 (|p| < 2^62), so
+// hi + k stays in int32 whenever |k| <= 2^30: together with 1 <= sh <= 30
+// that is the form's domain (RequantOdd::ok).  Equal to requant1 there.
+struct RequantOdd {
+  int32_t mo, k, sh;
+  bool ok;
+};
+I8_HD inline RequantOdd requant_odd_params(int32_t mult, int32_t shift, int32_t zp) {
+  const int s = shift < 0 ? 0 : (shift > 62 ? 62 : shift);
+  int t = 0;
+  uint32_t m = uint32_t(mult);
+  while (m != 0 && (m & 1u) == 0) {
+    m >>= 1;
+    ++t;
+  }
+  RequantOdd r;
+  r.mo = mult == 0 ? 0 : int32_t(int64_t(mult) >> t);
+  const int sh = mult == 0 ? 1 : s - t - 32;
+  r.ok = sh >= 1 && sh <= 30;
+  const int64_t k = r.ok ? (int64_t(1) << (sh - 1)) + int64_t(zp) * (int64_t(1) << sh) : 0;
+  r.ok = r.ok && k >= -(int64_t(1) << 30) && k <= (int64_t(1) << 30);
+  r.k = r.ok ? int32_t(k) : 0;
+  r.sh = r.ok ? sh : 1;
+  return r;
+}
+I8_HD inline int32_t requant1_odd(int32_t acc, int32_t mo, int32_t k, int32_t sh) {
+  const int32_t hi = int32_t((int64_t(acc) * int64_t(mo)) >> 32);
+  const int32_t v = (hi + k) >> sh;
+  return v < -128 ? -128 : (v > 127 ? 127 : v);
+}
+
 #if defined(__HIPCC__)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -297,15 +346,13 @@ __device__ __forceinline__ uint32_t requant4(v4i acc, v4i mult, v4i shift, int32
   return packed;
 }
 
-// requant4 through requant1_short (am, hh, sh from requant_short_*); the
+// requant4 through requant1_odd (mo, k, sh from requant_odd_params); the
 // low bytes are gathered with two byte permutes: v_perm_b32 selector bytes
 // 0-3 pick from its second operand, 4-7 from its first, 0x0c gives zero.
-__device__ __forceinline__ uint32_t requant4_short(v4i acc, v4i am, v4i mult, v4i hh, v4i sh,
-                                                   int32_t zp) {
+__device__ __forceinline__ uint32_t requant4_odd(v4i acc, v4i mo, v4i k, v4i sh) {
   int32_t y[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    y[e] = requant1_short(acc[e], uint32_t(am[e]), mult[e], uint32_t(hh[e]), uint32_t(sh[e]), zp);
+  for (int e = 0; e < 4; ++e) y[e] = requant1_odd(acc[e], mo[e], k[e], sh[e]);
   const uint32_t lo = __builtin_amdgcn_perm(uint32_t(y[1]), uint32_t(y[0]), 0x0c0c0400u);
   const uint32_t hi = __builtin_amdgcn_perm(uint32_t(y[3]), uint32_t(y[2]), 0x0c0c0400u);
   return __builtin_amdgcn_perm(hi, lo, 0x05040100u);

@@ -67,7 +67,7 @@ __device__ __forceinline__ v4i pw_mfma(v4i a, v4i b, v4i c) {
 // | sign bit of mult, so that two registers per channel carry the constants:
 // shifts take the low five bits of shx (sh is 1..30), hh = 2^(sh - 1) is
 // formed on the fly, and the sign of acc xor mult is that of acc xor shx.
-// Four channels packed as int8 like requant4_short.
+// Four channels packed as int8 like requant4_odd (i8conv_device.hpp).
 __device__ __forceinline__ uint32_t pw_requant4_short(v4i acc, v4i am, v4i shx, int32_t zp) {
   int32_t y[4];
 #pragma unroll

@@ -174,12 +174,12 @@ struct PassState {
   __amdgpu_buffer_rsrc_t yr;
   uint32_t voff[NFR];
   uint32_t row_stride;
-  // kQ: this lane's four channels' multiplier and shift; |multiplier|,
-  // 2^(shift - 33) and shift - 32 for requant4_short, which the wave takes
-  // when all its channels have shift >= 33 and |zero point| <= 2^30 (qshort)
+  // kQ: this lane's four channels' multiplier and shift, and their odd
+  // multiplier, k and sh for requant4_odd, which the wave takes when every
+  // one of its channels is in that form's domain (qodd; else requant4)
   v4i qm, qs;
-  v4i qam, qhh, qsh;
-  bool qshort;
+  v4i qmo, qk, qsh;
+  bool qodd;
 
   // steps of a walk that test each row's chunk flags before the walk tests
   // its last chunk's
@@ -250,12 +250,13 @@ struct PassState {
   __device__ __forceinline__ void step(const PassArgs &p, int rows_out, int m_row0, int oc0,
                                        int lane) {
     // Output row IR - 3 was completed by the previous row's MFMAs.
-    // kStoreFull: its two stores go between this row's MFMAs, after the
-    // sixth, by which time the MFMAs that completed it have drained.
+    // kStoreFull: its two stores (with kQ, requantized in the odd form) go
+    // between this row's MFMAs, after the sixth, by which time the MFMAs
+    // that completed it have drained.
     // Otherwise (a branch per row: element stores, or a block with fewer
     // rows than the walk) it is stored first thing.
     constexpr bool kStoreHere = G + NG == kGroups && IR >= OLO + 3;
-    constexpr bool kInStep = kStoreHere && !kQ && kMode == kStoreFull;
+    constexpr bool kInStep = kStoreHere && kMode == kStoreFull;
     if constexpr (kStoreHere && !kInStep)
       store_row<IR - 3>(p, kMode != kStoreElem, rows_out, m_row0, oc0, lane);
     v4i cur[NG][3][NFR];
@@ -298,7 +299,15 @@ struct PassState {
         }
       }
     }
-    if constexpr (kInStep) {
+    if constexpr (kInStep && kQ) {
+      // kStoreFull with kQ: the wave takes the odd-multiplier form (qodd),
+      // whose ~5 VALU operations per value the compiler spreads between
+      // the MFMAs like the reads
+#pragma unroll
+      for (int j = 0; j < NFR; ++j)
+        __builtin_amdgcn_raw_buffer_store_b32(requant4_odd(acc[IR - 3][j], qmo, qk, qsh), yr,
+                                              voff[j], (IR - 3) * row_stride, 0);
+    } else if constexpr (kInStep) {
 #pragma unroll
       for (int j = 0; j < NFR; ++j)
         __builtin_amdgcn_raw_buffer_store_b128(acc[IR - 3][j], yr, voff[j],
@@ -315,22 +324,22 @@ struct PassState {
   // == 0 (and an aligned output): one buffer store per fragment at a scalar
   // row offset, no address arithmetic: 16 bytes of int32 (write-through,
   // kStoreThrough), or with kQ the four requantized int8 values as one
-  // dword (evict-first, kStoreStream: a wave writes 16 bytes of a pixel's
-  // line, and the L2 merges the four waves' pieces before writing it);
-  // otherwise element stores.
+  // dword (an ordinary store: a wave writes 16 bytes of a pixel's line, and
+  // the L2 merges the four waves' pieces before writing it; 28x28x128 int8
+  // output with the odd form: 7.35 us per launch, against 7.5 written
+  // through and 8.2 evict-first, same box); otherwise element stores.
   template <int O>
   __device__ __forceinline__ void store_row(const PassArgs &p, bool vec, int rows_out, int m_row0,
                                             int oc0, int lane) {
     if (O >= rows_out) return;
     if constexpr (kQ) {
       if (vec) {
-        // qshort is uniform over the wave: a scalar branch
-        if (qshort) {
+        // qodd is uniform over the wave: a scalar branch
+        if (qodd) {
 #pragma unroll
           for (int j = 0; j < NFR; ++j)
-            __builtin_amdgcn_raw_buffer_store_b32(
-                requant4_short(acc[O][j], qam, qm, qhh, qsh, p.qzp), yr, voff[j], O * row_stride,
-                kStoreStream);
+            __builtin_amdgcn_raw_buffer_store_b32(requant4_odd(acc[O][j], qmo, qk, qsh), yr,
+                                                  voff[j], O * row_stride, 0);
         } else {
 #pragma unroll
           for (int j = 0; j < NFR; ++j)
@@ -480,7 +489,8 @@ struct CopySchedule {
 // then the walk(s) over the input rows, then the last row's store.
 template <int R, int NFR, int NG, bool kQ, int OLO, int OHI>
 __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, int wave, int lane,
-                                         int b, int oy0, int rows_out, int tile_n) {
+                                         int b, int oy0, int rows_out, int tile_n, v4i qm,
+                                         v4i qs) {
   PassState<R, NFR, NG, kQ, OLO, OHI> st;
   st.bias_lds = smem + wave * 256;
   st.planes = smem + kHaloBiasLds;
@@ -519,24 +529,19 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
                      : kOutOfRange;
   }
   if constexpr (kQ) {
-    // channels past N read as zero (their values are never stored)
-    const auto mr = make_rsrc(p.qmult, uint32_t(p.gemm_n) * 4u);
-    const auto sr = make_rsrc(p.qshift, uint32_t(p.gemm_n) * 4u);
+    st.qm = qm;
+    st.qs = qs;
+    bool ok = true;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      st.qm[e] = __builtin_amdgcn_raw_buffer_load_b32(mr, uint32_t(oc0 + e) * 4u, 0, 0);
-      st.qs[e] = __builtin_amdgcn_raw_buffer_load_b32(sr, uint32_t(oc0 + e) * 4u, 0, 0);
-    }
-    bool ok = requant_short_zp_ok(p.qzp);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
+      const RequantOdd o = requant_odd_params(st.qm[e], st.qs[e], p.qzp);
       // channels past N are never stored: they do not hold the wave back
-      ok = ok && (oc0 + e >= p.gemm_n || requant_short_ok(st.qs[e]));
-      st.qam[e] = int32_t(requant_short_am(st.qm[e]));
-      st.qhh[e] = int32_t(requant_short_hh(st.qs[e]));
-      st.qsh[e] = int32_t(requant_short_sh(st.qs[e]));
+      ok = ok && (oc0 + e >= p.gemm_n || o.ok);
+      st.qmo[e] = o.mo;
+      st.qk[e] = o.k;
+      st.qsh[e] = o.sh;
     }
-    st.qshort = __builtin_amdgcn_ballot_w64(!ok) == 0;
+    st.qodd = __builtin_amdgcn_ballot_w64(!ok) == 0;
   }
 
   // The walk specialised for the (uniform) store path: each copy holds only
@@ -548,7 +553,7 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
     if constexpr (NG == 1) st.template walk<1, M>(p, rows_out, m_row0, oc0, lane);
     st.template store_row<OHI - 1>(p, M != kStoreElem, rows_out, m_row0, oc0, lane);
   };
-  if (vec && !kQ && rows_out >= OHI)
+  if (vec && rows_out >= OHI && (!kQ || st.qodd))
     walks(std::integral_constant<int, kStoreFull>{});
   else if (vec)
     walks(std::integral_constant<int, kStoreVec>{});
@@ -599,6 +604,26 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   const uint32_t flags = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
   const int nchunks = (kGroups / NG) * p.rows_in;
   constexpr int kSplit = split_rows(R, NG, kQ);
+
+  // kQ: the multipliers and shifts of this lane's four output channels, for
+  // every wave that walks rows, loaded first thing (the walk needs them
+  // before its first row).  Channels past N read as zero (their values are
+  // never stored).  Staged through LDS with the bias instead (16 active
+  // lanes per copy wave) they measured 7.43-7.55 against 7.16-7.18 us per
+  // launch (28x28x128, int8 output, same box).
+  v4i qm{0, 0, 0, 0}, qs{0, 0, 0, 0};
+  if constexpr (kQ) {
+    if (!copier || kSplit > 0) {
+      const int oc0 = tile_n + wave * 16 + 4 * (lane >> 4);
+      const auto mr = make_rsrc(p.qmult, uint32_t(p.gemm_n) * 4u);
+      const auto sr = make_rsrc(p.qshift, uint32_t(p.gemm_n) * 4u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qm[e] = __builtin_amdgcn_raw_buffer_load_b32(mr, uint32_t(oc0 + e) * 4u, 0, 0);
+        qs[e] = __builtin_amdgcn_raw_buffer_load_b32(sr, uint32_t(oc0 + e) * 4u, 0, 0);
+      }
+    }
+  }
 
   if (wave_id == 0 && lane < nchunks) {
     // every flag starts at zero before any copy can land
@@ -672,12 +697,12 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     // MFMA wave's 16 channels (its copies have landed; the chunk flags say
     // when the other copy waves' have).
     if constexpr (kSplit > 0)
-      run_walk<R, NFR, NG, kQ, kSplit, R>(p, smem, wave, lane, b, oy0, rows_out, tile_n);
+      run_walk<R, NFR, NG, kQ, kSplit, R>(p, smem, wave, lane, b, oy0, rows_out, tile_n, qm, qs);
     return;
   }
   flag_barrier();
   run_walk<R, NFR, NG, kQ, 0, (kSplit > 0 ? kSplit : R)>(p, smem, wave, lane, b, oy0, rows_out,
-                                                          tile_n);
+                                                          tile_n, qm, qs);
 }
 
 

@@ -1,5 +1,5 @@
 """python -m int8_kernel_lab_amd.timeline build
-python -m int8_kernel_lab_amd.timeline run [LAYER] [--steps K] [--json PATH]
+python -m int8_kernel_lab_amd.timeline run [LAYER] [--steps K] [--requant] [--json PATH]
 
 build: compiles the stamped copies of the row kernel with copy waves and the
 deep-channel split-K into timeline/_build/libi8conv_timeline.so (the library
@@ -8,9 +8,10 @@ itself must be built first: make -C int8_kernel_lab_amd/csrc).
 run: on the GPU, launches LAYER (a row of workloads/baseline.csv, default
 cfg2_resnet_3x3_s1) with its dispatched kernel through the stamped library,
 checks it bit-exact against the oracle, times it like bench.py (graph region,
-then K launches enqueued on a stream, whose last launch leaves the stamps)
-and prints each stamp's spread over waves: min / median / max microseconds
-after the launch's first wave started.
+then K launches enqueued on a stream, whose last launch leaves the stamps;
+with --requant, int8 output timed like bench.py --requant) and prints each
+stamp's spread over waves: min / median / max microseconds after the
+launch's first wave started.
 """
 from __future__ import annotations
 
@@ -103,8 +104,19 @@ def _child(args):
     x, w, b = lab.make_case_data(shape)
     expected = oracle.conv(shape, x, w, b)
     xb, wb, bb = (lab.DeviceBuffer.from_array(v) for v in (x, w, b))
-    yb = lab.DeviceBuffer(4 * g.output_elements)
-    ws_n = lab.workspace_bytes(kernel, shape)
+    if args.requant:
+        # bench.py --requant's multipliers, shifts and zero point
+        rng = np.random.default_rng(1)
+        mult = rng.integers(2 ** 30, 2 ** 31, size=shape.k).astype(np.int32)
+        shift = rng.integers(50, 54, size=shape.k).astype(np.int32)
+        expected = oracle.requantize(expected, mult, shift, 3)
+        mb, sb = lab.DeviceBuffer.from_array(mult), lab.DeviceBuffer.from_array(shift)
+        yb = lab.DeviceBuffer(g.output_elements)
+        ws_n = lab.requant_workspace_bytes(shape)
+    else:
+        mb = sb = None
+        yb = lab.DeviceBuffer(4 * g.output_elements)
+        ws_n = lab.workspace_bytes(kernel, shape)
     ws = lab.DeviceBuffer(ws_n) if ws_n else None
     count = MAX_WORKGROUPS * instrument.WAVES * instrument.SLOTS
     tl = lab.DeviceBuffer(8 * count)
@@ -115,19 +127,30 @@ def _child(args):
     print(f"timeline: {args.layer} {shape} kernel={kernel} ({lab.describe(kernel, shape)})",
           flush=True)
     yb.fill(0xA5)
-    lab.launch(kernel, shape, xb, wb, bb, yb, ws, ws_n)
+    if args.requant:
+        lab.launch_requant(shape, xb, wb, bb, mb, sb, 3, yb, ws, ws_n)
+    else:
+        lab.launch(kernel, shape, xb, wb, bb, yb, ws, ws_n)
     lab.synchronize()
-    got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
+    got = yb.download(np.int8 if args.requant else np.int32,
+                      g.output_elements).reshape(shape.output_shape)
     exact = bool(np.array_equal(got, expected))
     expired = lab.wait_expired()
     print(f"bit-exact vs oracle: {exact}; a bounded wait gave up: {expired}", flush=True)
-    t = lab.measure_graph(kernel, shape, xb, wb, bb, yb, ws, ws_n, warmup=20, min_warmup_ms=100,
-                          iterations=args.steps, launches_per_graph=args.steps, poison_byte=0xA5)
+    result = {"layer": args.layer, "kernel": kernel, "output": "int8" if args.requant else "int32",
+              "bit_exact": exact, "wait_gave_up": expired, "steps": args.steps}
+    if args.requant:
+        # events around K back-to-back launches (bench.py --requant)
+        _, mean_ms = lab.measure_requant(shape, xb, wb, bb, mb, sb, 3, yb, ws, ws_n, warmup=20,
+                                         iterations=args.steps)
+        result["stream_us_per_launch"] = round(mean_ms * 1e3, 3)
+    else:
+        t = lab.measure_graph(kernel, shape, xb, wb, bb, yb, ws, ws_n, warmup=20,
+                              min_warmup_ms=100, iterations=args.steps,
+                              launches_per_graph=args.steps, poison_byte=0xA5)
+        result["graph_us_per_launch"] = round(t["mean_ms"] * 1e3, 3)
+        result["stream_us_per_launch"] = round(t["stream_ms"] * 1e3, 3)
     lab.synchronize()
-    result = {"layer": args.layer, "kernel": kernel, "bit_exact": exact, "wait_gave_up": expired,
-              "graph_us_per_launch": round(t["mean_ms"] * 1e3, 3),
-              "stream_us_per_launch": round(t["stream_ms"] * 1e3, 3),
-              "steps": args.steps}
     stamps = tl.download(np.uint64, count).reshape(MAX_WORKGROUPS, instrument.WAVES,
                                                     instrument.SLOTS)
     for name in ("kernel_rowpass.hip", "kernel_deepk.hip"):
@@ -137,10 +160,10 @@ def _child(args):
             result["stamped_kernel"] = name
             result.update(a)
             break
-    for buf in (xb, wb, bb, yb, ws, tl):
+    for buf in (xb, wb, bb, yb, ws, tl, mb, sb):
         if buf is not None:
             buf.close()
-    print(f"graph {result['graph_us_per_launch']} us/launch, stream "
+    print(f"graph {result.get('graph_us_per_launch', '-')} us/launch, stream "
           f"{result['stream_us_per_launch']} us/launch (K = {args.steps})")
     if "stamped_kernel" not in result:
         print("no stamps: the dispatched kernel is neither stamped kernel, or its grid "
@@ -167,6 +190,8 @@ def main(argv=None) -> int:
     run.add_argument("layer", nargs="?", default="cfg2_resnet_3x3_s1")
     run.add_argument("--steps", type=int, default=20)
     run.add_argument("--json")
+    run.add_argument("--requant", action="store_true",
+                     help="int8 output (launch_requant), timed like bench.py --requant")
     run.add_argument("--child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
     if args.cmd == "build":
@@ -181,7 +206,7 @@ def main(argv=None) -> int:
     path = os.pathsep.join(p for p in (ROOT, os.environ.get("PYTHONPATH")) if p)
     env = dict(os.environ, I8CONV_LIBRARY=instrument.LIBRARY, PYTHONPATH=path)
     cmd = [sys.executable, "-u", "-m", "int8_kernel_lab_amd.timeline", "run", args.layer,
-           "--steps", str(args.steps), "--child"]
+           "--steps", str(args.steps), "--child"] + (["--requant"] if args.requant else [])
     if args.json:
         cmd += ["--json", os.path.abspath(args.json)]
     return subprocess.run(cmd, env=env).returncode

@@ -1,9 +1,9 @@
-// Host build of the kernels' requantization (requant1 and requant1_short in
-// i8conv_device.hpp), driven by tests/test_requant.py: reads "acc mult shift
-// zp" lines on stdin and prints, per line, requant1's result and the short
-// form's (or requant1's again where the short form does not apply), which
-// the test compares with the CPU checker's restatement and with exact
-// rational arithmetic.
+// Host build of the kernels' requantization (requant1, requant1_short and
+// requant1_odd in i8conv_device.hpp), driven by tests/test_requant.py: reads
+// "acc mult shift zp" lines on stdin and prints, per line, requant1's
+// result, the short form's and the odd-multiplier form's (each form
+// requant1's again where it does not apply) and 1 or 0 for whether the odd
+// form applies, which the test compares with exact rational arithmetic.
 #include <stdint.h>
 #include <stdio.h>
 
@@ -19,7 +19,9 @@ int main() {
             ? i8conv::requant1_short(a, i8conv::requant_short_am(m), m, i8conv::requant_short_hh(s),
                                      i8conv::requant_short_sh(s), z)
             : full;
-    printf("%d %d\n", full, brief);
+    const i8conv::RequantOdd o = i8conv::requant_odd_params(m, s, z);
+    const int32_t odd = o.ok ? i8conv::requant1_odd(a, o.mo, o.k, o.sh) : full;
+    printf("%d %d %d %d\n", full, brief, odd, o.ok ? 1 : 0);
   }
   return 0;
 }

@@ -386,23 +386,28 @@ def test_pointwise_requant_unaligned_output_takes_the_unfused_path():
     np.testing.assert_array_equal(raw[4:count + 4].reshape(exp.shape), exp)
 
 
-SHORT_FORM = {
-    # every wave takes the short form (shift >= 33, |zp| <= 2^30) with
-    # multipliers of both signs; quotients spread over the int8 range
-    "short": (-3, ()),
-    # two waves' channels leave its domain (shift 32 and 20): those waves
-    # take the general form, the rest the short one
-    "mixed": (-3, ((77, 32), (5, 20))),
-    # zero point at the short form's limit
-    "zp_limit": (-(2 ** 30), ()),
-    # zero point just outside it: every wave takes the general form
-    "zp_outside": (2 ** 30 + 1, ()),
+FUSED_FORMS = {
+    # the row kernel's epilogue takes the odd-multiplier form per wave when
+    # all of its channels are in that form's domain (requant_odd_params):
+    # here every wave but the one holding channel 9 (mult -2^31: 31
+    # trailing zeros leave s' below 33), which takes the general form;
+    # multipliers of both signs, quotients spread over the int8 range
+    "odd": (-3, (), False),
+    # two more waves' channels leave the domain (shift 32 and 20)
+    "mixed": (-3, ((77, 32), (5, 20)), False),
+    # multipliers with 0..8 trailing zeros and shifts raised to match, so the
+    # form's normalization (mult = mo 2^t, s' = s - t) decides every value
+    "trailing_zeros": (-3, (), True),
+    # zero points that put k = 2^(sh-1) + zp 2^sh outside +-2^30: every wave
+    # takes the general form
+    "zp_limit": (-(2 ** 30), (), False),
+    "zp_outside": (2 ** 30 + 1, (), False),
 }
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("variant", sorted(SHORT_FORM))
-def test_fused_requant_short_form_bit_exact(variant):
+@pytest.mark.parametrize("variant", sorted(FUSED_FORMS))
+def test_fused_requant_forms_bit_exact(variant):
     from tests.conftest import say
     shape = _baseline("cfg2_resnet_3x3_s1")
     assert lab.requant_fused(shape)
@@ -412,13 +417,17 @@ def test_fused_requant_short_form_bit_exact(variant):
             * rng.choice([-1, 1], size=shape.k)).astype(np.int32)
     mult[9] = -(2 ** 31)
     shift = rng.integers(44, 47, size=shape.k).astype(np.int32)
-    zp, general = SHORT_FORM[variant]
+    zp, general, trailing = FUSED_FORMS[variant]
+    if trailing:
+        t = rng.integers(0, 9, size=shape.k)
+        mult = ((mult.astype(np.int64) >> 8) << t).astype(np.int32)   # |mult| < 2^31
+        shift = (shift - 8 + t).astype(np.int32)
     for ch, sh in general:
         shift[ch] = sh
-    say(f"[gpu] fused requant short form {variant}")
+    say(f"[gpu] fused requant form {variant}")
     got = lab.conv2d_requant(x, w, b, mult, shift, zp, shape)
     exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, zp)
-    if variant in ("short", "mixed"):
+    if variant in ("odd", "mixed", "trailing_zeros"):
         assert len(np.unique(exp)) > 200       # the quotients reach most int8 values
     np.testing.assert_array_equal(got, exp)
 
@@ -464,13 +473,42 @@ def test_kernel_requant_function_matches_oracle_on_host(tmp_path):
     mult[424:1400] = rng.integers(-(2 ** 31), 2 ** 31, size=976)
     shift[424:1400] = rng.integers(33, 70, size=976)
     zp[424:1400] = rng.integers(-(2 ** 30), 2 ** 30 + 1, size=976)
+    # the odd-multiplier form's edges: multipliers with trailing zeros, the
+    # shift at both ends of 1 <= sh <= 30, k at +-2^30, negative products
+    # just past a multiple of 2^32, the extreme accumulators, mult 0 and
+    # -2^31 (outside the form: t = 31)
+    e = 1400
+    rows = [(-1, 2 ** 31 - 1, 33, 0), (1, 2 ** 31 - 1, 33, 0), (-(2 ** 31), 2 ** 31 - 1, 33, 0),
+            (-(2 ** 31), 2 ** 31 - 1, 62, 0), (2 ** 31 - 1, -(2 ** 31 - 1), 33, 5),
+            (-(2 ** 31), -(2 ** 31 - 1), 34, -7), (12345, 3 << 20, 53, 1), (-12345, 3 << 20, 53, 1),
+            (-(2 ** 31), 3 << 20, 53, 0), (2 ** 31 - 1, 5 << 28, 62, 0), (-77, 5 << 28, 62, 0),
+            (-3, 1, 33, 2 ** 29 - 1), (3, -1, 33, -(2 ** 29)), (3, 1, 33, 2 ** 29),
+            (-(2 ** 31), 1, 62, 0), (2 ** 31 - 1, 1, 62, 0), (-5, 7, 62, 0), (5, -7, 62, 0),
+            (99, 0, 40, -3), (-99, 0, 40, 127), (100, -(2 ** 31), 62, 0), (-100, 2 ** 30, 62, 0),
+            (-100, 2 ** 30, 63, 0), (2 ** 20, 2 ** 31 - 1, 51, 0), (-(2 ** 20), 2 ** 31 - 1, 51, 0),
+            (-(2 ** 20) - 1, 2 ** 31 - 3, 51, 0), (2 ** 26, 2 ** 30 + 1, 48, 3),
+            (-(2 ** 26), 2 ** 30 + 1, 48, 3), (-(2 ** 26), 2 ** 30 + 1, 48, -128),
+            (2 ** 30, 2 ** 31 - 1, 34, 127)]
+    for i, (a, m, sv, z) in enumerate(rows):
+        acc[e + i], mult[e + i], shift[e + i], zp[e + i] = a, m, sv, z
     text = "\n".join(f"{a} {m} {s} {z}" for a, m, s, z in zip(acc, mult, shift, zp))
     out = subprocess.run([str(exe)], input=text, text=True, capture_output=True, check=True)
-    got = np.array([int(v) for v in out.stdout.split()], dtype=np.int64).reshape(-1, 2)
+    got = np.array([int(v) for v in out.stdout.split()], dtype=np.int64).reshape(-1, 4)
     assert got.shape[0] == n
     short = (shift >= 33) & (np.abs(zp) <= 2 ** 30)
     assert short.sum() > 1000
+    # the odd-multiplier form's domain: 1 <= min(shift, 62) - t - 32 <= 30
+    # (t = trailing zeros of mult) and |2^(sh-1) + zp 2^sh| <= 2^30
+    sc = np.clip(shift, 0, 62)
+    tz = np.array([(int(m) & -int(m)).bit_length() - 1 if m else 0 for m in mult])
+    sh = np.where(mult == 0, 1, sc - tz - 32)
+    kk = [(1 << (int(h) - 1)) + int(z) * (1 << int(h)) if 1 <= h <= 30 else None
+          for h, z in zip(sh, zp)]
+    odd = np.array([k is not None and abs(k) <= 2 ** 30 for k in kk])
+    np.testing.assert_array_equal(got[:, 3], odd.astype(np.int64))
+    assert odd.sum() > 1000
     for i in range(n):
         want = exact_requant(int(acc[i]), int(mult[i]), int(shift[i]), int(zp[i]))
         assert got[i, 0] == want, (i, acc[i], mult[i], shift[i], zp[i], got[i], want)
         assert got[i, 1] == want, ("short", i, acc[i], mult[i], shift[i], zp[i], got[i], want)
+        assert got[i, 2] == want, ("odd", i, acc[i], mult[i], shift[i], zp[i], got[i], want)
