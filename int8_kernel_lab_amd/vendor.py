@@ -55,6 +55,9 @@ def hipblaslt_gemm(shape, warmup: int = 20, iterations: int = 101) -> Dict[str, 
     import int8_kernel_lab_amd as lab
 
     if not torch.cuda.is_available():
+        # also the case where the lab's library initialised the GPU first:
+        # both load libamdhip64.so.7, and torch needs its own copy to be the
+        # one the process loaded (import torch before the lab's first GPU call)
         return {"hipblaslt_ms": "", "hipblaslt_correct": "", "hipblaslt_contract": "no gpu"}
     x, w, b = lab.make_case_data(shape)
     m = shape.n * shape.h * shape.w
@@ -69,10 +72,17 @@ def hipblaslt_gemm(shape, warmup: int = 20, iterations: int = 101) -> Dict[str, 
     y_lab = torch.empty((m, shape.k), dtype=torch.int32, device="cuda")
     xd = torch.from_numpy(x).cuda()
     wd = torch.from_numpy(w).cuda()
+    # the dispatched kernel's workspace (split-K partial sums on deep layers;
+    # torch's allocations are 256-byte aligned)
+    kernel = lab.dispatch(shape)
+    ws_n = lab.workspace_bytes(kernel, shape)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device="cuda") if ws_n else None
     torch.cuda.synchronize()
-    lab.launch(lab.dispatch(shape), shape, xd.data_ptr(), wd.data_ptr(), bias.data_ptr(),
-               y_lab.data_ptr(), None, 0)
+    lab.launch(kernel, shape, xd.data_ptr(), wd.data_ptr(), bias.data_ptr(), y_lab.data_ptr(),
+               ws.data_ptr() if ws is not None else None, ws_n)
     lab.synchronize()
+    if lab.wait_expired():
+        raise RuntimeError(f"{kernel}: a bounded wait gave up; the output is not to be trusted")
     correct = bool(torch.equal(y + bias, y_lab))
     for _ in range(warmup):
         torch._int_mm(a, wt)

@@ -8,6 +8,14 @@ import sys
 
 import pytest
 
+# torch before the library's first GPU call: both load libamdhip64.so.7, and
+# the first copy loaded serves the process; torch's own (the version it was
+# built for) must be that one for torch.cuda to see the GPU
+try:
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover - torch is part of the image
+    torch = None
+
 from tests.conftest import DRIVER, ROOT, say
 
 REF_COLUMNS = ["case", "n", "h", "w", "c", "k", "r", "s", "out_h", "out_w", "eligible_strip",
@@ -90,10 +98,17 @@ def test_vendor_miopen_matches_dispatched_kernel():
 
 
 @pytest.mark.gpu
-def test_vendor_hipblaslt_gemm_matches_dispatched_kernel():
+@pytest.mark.parametrize("case", ["small", "darknet_res_13_reduce"])
+def test_vendor_hipblaslt_gemm_matches_dispatched_kernel(case):
+    # darknet_res_13_reduce (1x1, C = 1024) dispatches split-K, whose
+    # launch needs a workspace of partial sums
     import int8_kernel_lab_amd as lab
     from int8_kernel_lab_amd import vendor
-    shape = lab.ConvShape(2, 28, 28, 64, 96, 1, 1, 0, 0, 1, 1, 1, 1)
+    if case == "small":
+        shape = lab.ConvShape(2, 28, 28, 64, 96, 1, 1, 0, 0, 1, 1, 1, 1)
+    else:
+        shape = lab.load_case(os.path.join(lab.WORKLOADS_DIR, "reference.csv"), case)
+        assert lab.workspace_bytes(lab.dispatch(shape), shape) > 0
     say(f"[gpu] torch._int_mm vs dispatch on {shape}")
     got = vendor.hipblaslt_gemm(shape, warmup=1, iterations=3)
     assert got["hipblaslt_correct"] == 1, got
