@@ -77,27 +77,20 @@ constexpr int walk_groups(int nfr) { return nfr == 4 ? 1 : 2; }
 // count; 16-byte stores of a block that has all the walk's rows (no branch).
 constexpr int kStoreElem = 0, kStoreVec = 1, kStoreFull = 2;
 
-// Everything the kernel reads; loaded into SGPRs in one batch.
+// The arguments of the walk (the copy waves' come preloaded: PreGeo and
+// the kernel's leading pointers, below).
 struct PassArgs {
-  const int8_t *x;
-  const int8_t *w;
-  const int32_t *bias;
   int32_t *y;
-  uint32_t x_bytes, w_bytes;
   uint32_t y_bytes;  // output bytes (< 2^31: checked at launch)
   // requantized int8 output (kQ instances): per-channel multiplier and
   // shift, zero point, output (y_bytes then counts int8 bytes)
   const int32_t *qmult, *qshift;
   int8_t *qy;
   int32_t qzp;
-  int n, h, wd, c, pad_h, pad_w;
-  int out_h, out_w, gemm_n, gemm_k;
-  int hp, wp;        // padded rows per image, padded columns
+  int out_h, out_w, gemm_n;
   int plane_copies;  // 1 KB copies per plane: ceil(wp * kUnits / 64)
   int rows_in;       // input rows per block: R + 2
-  int blocks, tiles_n;
   int spin_limit;    // polls of a bounded chunk wait (wait_spin_limit())
-  FastDiv3 div_plane_copies, div_hp, div_blocks, div_tiles_n;
 };
 
 // Cross-wave signals in LDS: flag words set by LDS-DMA flag copies behind
@@ -573,11 +566,22 @@ constexpr int split_rows(int R, int NG, bool kQ) {
   return kQ && NG == 2 && R >= 4 ? (R + 2) / 2 : 0;
 }
 
+// The kernel's leading arguments arrive preloaded in SGPRs (this file is
+// built with -amdgpu-kernarg-preload-count=7: seven arguments, ten words):
+// the base pointers of input, filter and bias and four words of the
+// layer's geometry (n; h | wd << 16;
+// pad_h | pad_w << 8 | blocks << 16, the row blocks per image; the output
+// channels), which is everything the copy waves need to issue their
+// copies.  The rest of the arguments (PassArgs) are loaded from the
+// kernel-argument segment as usual, a cold scalar round trip (~0.3 us after
+// a launch enqueued on a stream) that the MFMA waves take while the first
+// chunk lands.  The grid is (channel tiles, row blocks, images).
 template <int R, int NFR, int NG, bool kQ>
-__global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg) {
+__global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(
+    const int8_t *x_pre, const int8_t *w_pre, const int32_t *bias_pre, uint32_t n_pre,
+    uint32_t hw_pre, uint32_t pads_pre, uint32_t gemm_n_pre, PassArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-  const PassArgs p = p_arg;
-  pin_sgprs(p);
+  const PassArgs &p = p_arg;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -586,44 +590,59 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   // the MFMA wave this wave is, 0..3 (or copies the filter halves and bias for)
   const int wave = wave_id & 3;
 
-  const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
-  const int tn = int(blockIdx.x) - rest * p.tiles_n;
-  const int b = int(fast_div(uint32_t(rest), p.div_blocks));
-  const int q = rest - b * p.blocks;
-  const int oy0 = int((int64_t(q) * p.out_h) / p.blocks);
-  const int rows_out = int((int64_t(q + 1) * p.out_h) / p.blocks) - oy0;  // <= R
+  // geometry from the preloaded words (c == 128, 3x3, stride 1, dilation 1)
+  const int n = int(n_pre);
+  const int h = int(hw_pre & 0xffffu), wd = int(hw_pre >> 16);
+  const int pad_h = int(pads_pre & 0xffu), pad_w = int((pads_pre >> 8) & 0xffu);
+  const int blocks = int(pads_pre >> 16);
+  const int gemm_n = int(gemm_n_pre);
+  const int hp = h + 2 * pad_h;
+  const int out_h = hp - 2;
+  const int plane_copies = ((wd + 2 * pad_w) * kUnits + 63) / 64;
+  constexpr int kRowsIn = R + 2;
+  constexpr int kGemmK = 9 * 64 * kGroups;
+
+  // grid: (channel tiles, row blocks, images)
+  const int tn = int(blockIdx.x);
+  const int q = int(blockIdx.y);
+  const int b = int(blockIdx.z);
+  // out_h < 2^16 and q < blocks <= out_h: the products fit in 32 bits
+  const int oy0 = int(uint32_t(q * out_h) / uint32_t(blocks));
+  const int rows_out = int(uint32_t((q + 1) * out_h) / uint32_t(blocks)) - oy0;  // <= R
   const int tile_n = tn * 64;
 
   // LDS: [bias, 256 B per wave][planes: group 0 rows, group 1 rows]
   //      [filter halves: 18 KB per wave][chunk flags: 16 B per chunk]
   const int8_t *bias_lds = smem + wave * 256;
   const int8_t *planes = smem + kHaloBiasLds;
-  const int plane_bytes = p.plane_copies * 1024;
-  const int8_t *ring = planes + kGroups * p.rows_in * plane_bytes;
+  const int plane_bytes = plane_copies * 1024;
+  const int8_t *ring = planes + kGroups * kRowsIn * plane_bytes;
   const int8_t *halves = ring + wave * kHalves * 1024;
   const uint32_t flags = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
-  const int nchunks = (kGroups / NG) * p.rows_in;
+  constexpr int nchunks = (kGroups / NG) * kRowsIn;
   constexpr int kSplit = split_rows(R, NG, kQ);
 
   // kQ: the multipliers and shifts of this lane's four output channels, for
-  // every wave that walks rows, loaded first thing (the walk needs them
-  // before its first row).  Channels past N read as zero (their values are
-  // never stored).  Staged through LDS with the bias instead (16 active
-  // lanes per copy wave) they measured 7.43-7.55 against 7.16-7.18 us per
-  // launch (28x28x128, int8 output, same box).
+  // every wave that walks rows, loaded before the walk (the MFMA waves
+  // first thing, the copy waves that walk rows once their copies are
+  // issued).  Channels past N read as zero (their values are never
+  // stored).  Staged through LDS with the bias instead (16 active lanes per
+  // copy wave) they measured 7.43-7.55 against 7.16-7.18 us per launch
+  // (28x28x128, int8 output, same box).
   v4i qm{0, 0, 0, 0}, qs{0, 0, 0, 0};
-  if constexpr (kQ) {
-    if (!copier || kSplit > 0) {
+  auto load_q = [&]() {
+    if constexpr (kQ) {
       const int oc0 = tile_n + wave * 16 + 4 * (lane >> 4);
-      const auto mr = make_rsrc(p.qmult, uint32_t(p.gemm_n) * 4u);
-      const auto sr = make_rsrc(p.qshift, uint32_t(p.gemm_n) * 4u);
+      const auto mr = make_rsrc(p.qmult, uint32_t(gemm_n) * 4u);
+      const auto sr = make_rsrc(p.qshift, uint32_t(gemm_n) * 4u);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         qm[e] = __builtin_amdgcn_raw_buffer_load_b32(mr, uint32_t(oc0 + e) * 4u, 0, 0);
         qs[e] = __builtin_amdgcn_raw_buffer_load_b32(sr, uint32_t(oc0 + e) * 4u, 0, 0);
       }
     }
-  }
+  };
+  if (!copier) load_q();
 
   if (wave_id == 0 && lane < nchunks) {
     // every flag starts at zero before any copy can land
@@ -632,16 +651,16 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
   }
 
   if (copier) {
-    const v4u xd = make_desc(p.x, p.x_bytes);
-    const v4u wd = make_desc(p.w, p.w_bytes);
+    const v4u xd = make_desc(x_pre, uint32_t(n) * uint32_t(h) * uint32_t(wd) * uint32_t(64 * kGroups));
+    const v4u wd_desc = make_desc(w_pre, uint32_t(gemm_n) * uint32_t(kGemmK));
     const uint32_t planes_lds = lds_addr(planes);
     // filter halves for MFMA wave `wave`: lane -> filter row 16*wave +
     // lane/4 and 16-byte chunk lane%4, holding the chunk swz64 puts there
     const int frow = lane >> 2;
     const int fchunk = swz64_chunk(frow, lane & 3);
     const int oc_copy = tile_n + wave * 16 + frow;
-    const uint32_t fbase = oc_copy < p.gemm_n
-                               ? uint32_t(oc_copy) * uint32_t(p.gemm_k) + uint32_t(16 * fchunk)
+    const uint32_t fbase = oc_copy < gemm_n
+                               ? uint32_t(oc_copy) * uint32_t(kGemmK) + uint32_t(16 * fchunk)
                                : kOutOfRange;
     const uint32_t halves_lds = lds_addr(halves);
     // Chunk (groups g0 .. g0 + ng - 1, row r): the bias (first chunk), the
@@ -650,33 +669,36 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     // plane; unit u of pixel pix is slot pix*kUnits + u (u >= 4: padding,
     // left out of range -> zeros).
     auto issue_chunk = [&](int g0, int r, int pw, int ng) {
-      if (g0 == 0 && r == 0) stage_bias<1>(p.bias, p.gemm_n, tile_n + wave * 16, bias_lds, lane);
+      if (g0 == 0 && r == 0) stage_bias<1>(bias_pre, gemm_n, tile_n + wave * 16, bias_lds, lane);
       for (int g = g0; g < g0 + ng; ++g) {
         if (r <= 2) {
 #pragma unroll
           for (int fx = 0; fx < 3; ++fx) {
             const int t = 3 * r + fx;
-            lds_copy16(wd, halves_lds + uint32_t((g * kTaps + t) * 1024),
+            lds_copy16(wd_desc, halves_lds + uint32_t((g * kTaps + t) * 1024),
                        fbase + uint32_t(t * 128 + g * 64));
           }
         }
       }
-      const int vr = b * p.hp + oy0 + r;
-      const int bb = int(fast_div(uint32_t(vr), p.div_hp));
-      const int iy = vr - bb * p.hp - p.pad_h;
-      const bool row_ok = bb < p.n && unsigned(iy) < unsigned(p.h);
+      // padded row oy0 + r of image b; the rows past the image (a block
+      // shorter than R at the bottom) fall into the next image's top rows
+      // (oy0 + r < 2 hp), which are read but feed no stored output
+      const int pr = oy0 + r;
+      const int bb = b + (pr >= hp ? 1 : 0);
+      const int iy = pr - (pr >= hp ? hp : 0) - pad_h;
+      const bool row_ok = bb < n && unsigned(iy) < unsigned(h);
       // modulo 2^32: exact wherever it is used (the sums below are in [0, 2^31))
-      const uint32_t row_off = uint32_t((bb * p.h + iy) * p.wd - p.pad_w) * uint32_t(p.c);
+      const uint32_t row_off = uint32_t((bb * h + iy) * wd - pad_w) * uint32_t(64 * kGroups);
       for (int g = g0; g < g0 + ng; ++g) {
         for (int i = 0; i < pw; ++i) {
           const int j = wave + 4 * i;
           const int slot = j * 64 + lane;
           const int pix = slot / kUnits;
           const int u = slot - pix * kUnits;
-          const bool ok = row_ok && u < 4 && unsigned(pix - p.pad_w) < unsigned(p.wd);
-          const uint32_t off = ok ? row_off + uint32_t(64 * g + pix * p.c + 16 * u) : kOutOfRange;
-          lds_copy16(xd, planes_lds + uint32_t((g * p.rows_in + r) * plane_bytes + j * 1024),
-                     off);
+          const bool ok = row_ok && u < 4 && unsigned(pix - pad_w) < unsigned(wd);
+          const uint32_t off =
+              ok ? row_off + uint32_t(64 * g + pix * 64 * kGroups + 16 * u) : kOutOfRange;
+          lds_copy16(xd, planes_lds + uint32_t((g * kRowsIn + r) * plane_bytes + j * 1024), off);
         }
       }
     };
@@ -688,7 +710,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     };
     // plane copies per row and group this wave issues: j = wave, wave + 4;
     // each schedule passes the workgroup barrier once (flag_barrier)
-    const int pw = p.plane_copies > wave ? (p.plane_copies - wave + 3) / 4 : 0;
+    const int pw = plane_copies > wave ? (plane_copies - wave + 3) / 4 : 0;
     if (pw == 0) CopySchedule<R, 0, NG>::run(issue_chunk, signal);
     else if (pw == 1) CopySchedule<R, 1, NG>::run(issue_chunk, signal);
     else CopySchedule<R, 2, NG>::run(issue_chunk, signal);
@@ -696,18 +718,31 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(PassArgs p_arg
     // With a split, the copy wave then walks the block's last rows for its
     // MFMA wave's 16 channels (its copies have landed; the chunk flags say
     // when the other copy waves' have).
-    if constexpr (kSplit > 0)
+    if constexpr (kSplit > 0) {
+      pin_sgprs(p);
+      load_q();
       run_walk<R, NFR, NG, kQ, kSplit, R>(p, smem, wave, lane, b, oy0, rows_out, tile_n, qm, qs);
+    }
     return;
   }
+  // the remaining arguments, in one batch, while the first chunk lands
+  pin_sgprs(p);
   flag_barrier();
   run_walk<R, NFR, NG, kQ, 0, (kSplit > 0 ? kSplit : R)>(p, smem, wave, lane, b, oy0, rows_out,
                                                           tile_n, qm, qs);
 }
 
 
+// The preloaded leading arguments of rowpass_kernel.
+struct PreArgs {
+  const int8_t *x;
+  const int8_t *w;
+  const int32_t *bias;
+  uint32_t n, hw, pads, gemm_n;
+};
+
 template <int R, int NFR, bool kQ>
-int launch_q(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
+int launch_q(const PreArgs &a, const PassArgs &h, dim3 grid, size_t lds, hipStream_t s) {
   auto kern = rowpass_kernel<R, NFR, walk_groups(NFR), kQ>;
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -718,7 +753,8 @@ int launch_q(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(2 * kThreads), lds, s, h);
+  hipLaunchKernelGGL(kern, grid, dim3(2 * kThreads), lds, s, a.x, a.w, a.bias, a.n, a.hw, a.pads,
+                     a.gemm_n, h);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error(std::string("row kernel with copy waves, launch: ") + hipGetErrorString(e));
@@ -728,9 +764,10 @@ int launch_q(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s) {
 }
 
 template <int R, int NFR>
-int launch_t(const PassArgs &h, size_t blocks, size_t lds, hipStream_t s, bool requant) {
-  return requant ? launch_q<R, NFR, true>(h, blocks, lds, s)
-                 : launch_q<R, NFR, false>(h, blocks, lds, s);
+int launch_t(const PreArgs &a, const PassArgs &h, dim3 grid, size_t lds, hipStream_t s,
+             bool requant) {
+  return requant ? launch_q<R, NFR, true>(a, h, grid, lds, s)
+                 : launch_q<R, NFR, false>(a, h, grid, lds, s);
 }
 
 }  // namespace
@@ -767,13 +804,21 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream, const Re
     set_error("row plan (copy waves) out of range");
     return I8CONV_BAD_ARGUMENT;
   }
+  if (a.h >= 65536 || a.wd >= 65536 || a.pad_h >= 256 || a.pad_w >= 256 || p.ranges >= 65536 ||
+      a.n >= 65536 || a.pad_h < 0 || a.pad_w < 0) {
+    set_error("row plan (copy waves): geometry beyond the packed kernel arguments");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  PreArgs pre;
+  pre.x = a.x;
+  pre.w = a.w;
+  pre.bias = a.bias;
+  pre.n = uint32_t(a.n);
+  pre.hw = uint32_t(a.h) | uint32_t(a.wd) << 16;
+  pre.pads = uint32_t(a.pad_h) | uint32_t(a.pad_w) << 8 | uint32_t(p.ranges) << 16;
+  pre.gemm_n = uint32_t(a.gemm_n);
   PassArgs h{};
-  h.x = a.x;
-  h.w = a.w;
-  h.bias = a.bias;
   h.y = a.y;
-  h.x_bytes = a.x_bytes;
-  h.w_bytes = a.w_bytes;
   h.y_bytes = uint32_t(int64_t(a.gemm_m) * a.gemm_n * (q ? 1 : 4));
   if (q) {
     h.qmult = q->mult;
@@ -781,34 +826,19 @@ int launch_rowpass(const ConvArgs &a, const PatchPlan &p, void *stream, const Re
     h.qy = q->y;
     h.qzp = q->zero_point;
   }
-  h.n = a.n;
-  h.h = a.h;
-  h.wd = a.wd;
-  h.c = a.c;
-  h.pad_h = a.pad_h;
-  h.pad_w = a.pad_w;
   h.out_h = a.out_h;
   h.out_w = a.out_w;
   h.gemm_n = a.gemm_n;
-  h.gemm_k = a.gemm_k;
-  h.hp = a.h + 2 * a.pad_h;
-  h.wp = wp;
   h.plane_copies = (wp * kUnits + 63) / 64;
   h.rows_in = R + 2;
-  h.blocks = p.ranges;
-  h.tiles_n = p.tiles_n;
   h.spin_limit = wait_spin_limit();
-  h.div_plane_copies = make_fastdiv3(uint32_t(h.plane_copies));
-  h.div_hp = make_fastdiv3(uint32_t(h.hp));
-  h.div_blocks = make_fastdiv3(uint32_t(h.blocks));
-  h.div_tiles_n = make_fastdiv3(uint32_t(h.tiles_n));
-  const size_t grid = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n);
+  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define I8_PASS_CASE(RR)                                                   \
-  if (R == RR) {                                                           \
-    if (nfr == 1) return launch_t<RR, 1>(h, grid, lds, s, q != nullptr);   \
-    if (nfr == 2) return launch_t<RR, 2>(h, grid, lds, s, q != nullptr);   \
-    if constexpr (RR <= 4) return launch_t<RR, 4>(h, grid, lds, s, q != nullptr); \
+#define I8_PASS_CASE(RR)                                                         \
+  if (R == RR) {                                                                 \
+    if (nfr == 1) return launch_t<RR, 1>(pre, h, grid, lds, s, q != nullptr);    \
+    if (nfr == 2) return launch_t<RR, 2>(pre, h, grid, lds, s, q != nullptr);    \
+    if constexpr (RR <= 4) return launch_t<RR, 4>(pre, h, grid, lds, s, q != nullptr); \
   }
   I8_PASS_CASE(1) I8_PASS_CASE(2) I8_PASS_CASE(3) I8_PASS_CASE(4)
   I8_PASS_CASE(5) I8_PASS_CASE(6) I8_PASS_CASE(7) I8_PASS_CASE(8)

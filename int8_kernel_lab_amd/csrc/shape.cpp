@@ -344,7 +344,10 @@ bool plan_row(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
   if (found && s.c == 128 && p->bn == 64 && rowpass_nfr(g.out_w) != 0 &&
       p->rows - 2 <= rowpass_max_rows(rowpass_nfr(g.out_w)) &&
       rowpass_lds_bytes(s.w + 2 * s.pad_w, p->rows - 2) <= size_t(kLdsBudget) &&
-      g.output_elements * 4 <= INT32_MAX)
+      g.output_elements * 4 <= INT32_MAX &&
+      // its geometry travels in packed preloaded argument words, its grid
+      // is (channel tiles, row blocks, images)
+      s.n < 65536 && s.h < 65536 && s.w < 65536 && s.pad_h < 256 && s.pad_w < 256)
     p->streamed = true;
   return found;
 }

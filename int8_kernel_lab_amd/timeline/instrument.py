@@ -24,7 +24,7 @@ WAVES = 16   # wave slots per workgroup in the stamp buffer
 SLOTS = 32   # stamp slots per wave
 
 # Row kernel with copy waves: slot -> meaning
-ROWPASS_SLOTS = {0: "wave start", 1: "arguments loaded", 31: "past the flag barrier",
+ROWPASS_SLOTS = {0: "wave start", 1: "MFMA wave: arguments loaded", 31: "past the flag barrier",
                  2: "copy wave: all copies issued", 3: "copy wave: copies landed",
                  27: "MFMA wave: walk start", 29: "MFMA wave: walk end",
                  30: "MFMA wave: stores drained"}
@@ -40,14 +40,16 @@ DEEPK_FRAG_SLOTS = {4 + i: f"MFMA wave: fragment {i} image ready" for i in range
 _STAMP = """
 __device__ __forceinline__ void tl_put(unsigned long long *tl, int slot, unsigned long long v) {
   if (tl && (threadIdx.x & 63) == 0 && (threadIdx.x >> 6) < %(waves)d)
-    tl[(blockIdx.x * %(waves)d + (threadIdx.x >> 6)) * %(slots)d + slot] = v;
+    tl[(((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * %(waves)d +
+        (threadIdx.x >> 6)) * %(slots)d + slot] = v;
 }
 __device__ __forceinline__ unsigned long long tl_now() { return __builtin_amdgcn_s_memrealtime(); }
 """ % {"waves": WAVES, "slots": SLOTS}
 
 ROWPASS_EDITS = [
-    ("  FastDiv3 div_plane_copies, div_hp, div_blocks, div_tiles_n;\n};",
-     "  FastDiv3 div_plane_copies, div_hp, div_blocks, div_tiles_n;\n  unsigned long long *tl;\n};"),
+    ("  int spin_limit;    // polls of a bounded chunk wait (wait_spin_limit())\n};",
+     "  int spin_limit;    // polls of a bounded chunk wait (wait_spin_limit())\n"
+     "  unsigned long long *tl;\n};"),
     ("constexpr int kStoreElem = 0, kStoreVec = 1, kStoreFull = 2;",
      "constexpr int kStoreElem = 0, kStoreVec = 1, kStoreFull = 2;\n" + _STAMP),
     ("      constexpr int fy_next = IR + 1 - OLO;",
@@ -63,8 +65,10 @@ ROWPASS_EDITS = [
      "    st.template store_row<OHI - 1>(p, M != kStoreElem, rows_out, m_row0, oc0, lane);\n"
      "    asm volatile(\"s_waitcnt vmcnt(0)\" ::: \"memory\");\n"
      "    tl_put(p.tl, 30, tl_now());\n  };"),
-    ("  const PassArgs p = p_arg;\n  pin_sgprs(p);\n",
-     "  const unsigned long long t_start = tl_now();\n  const PassArgs p = p_arg;\n  pin_sgprs(p);\n"
+    ("  const PassArgs &p = p_arg;\n",
+     "  const unsigned long long t_start = tl_now();\n  const PassArgs &p = p_arg;\n"),
+    ("  // the remaining arguments, in one batch, while the first chunk lands\n  pin_sgprs(p);\n",
+     "  // the remaining arguments, in one batch, while the first chunk lands\n  pin_sgprs(p);\n"
      "  tl_put(p.tl, 0, t_start);\n  tl_put(p.tl, 1, tl_now());\n"),
     ("  flag_barrier();\n  run_walk<",
      "  flag_barrier();\n  tl_put(p.tl, 31, tl_now());\n  run_walk<"),
@@ -73,15 +77,16 @@ ROWPASS_EDITS = [
      "    };",
      "    auto signal = [&](int c) {\n"
      "      if (lane == 0) lds_copy4(one, flags + 16u * uint32_t(c) + 4u * uint32_t(wave), 0u);\n"
-     "      if (c == 0) tl_put(p.tl, 31, tl_now());\n"
+     "      if (c == 0) { tl_put(p.tl, 31, tl_now()); tl_put(p.tl, 0, t_start); }\n"
      "      if (c == nchunks - 1) tl_put(p.tl, 2, tl_now());\n"
      "    };"),
     ("    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n    // With a split",
      "    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n"
      "    tl_put(p.tl, 3, tl_now());\n    // With a split"),
-    ("  const size_t grid = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n);\n",
-     "  const size_t grid = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n);\n"
-     "  h.tl = grid <= size_t(g_i8_timeline_wgs) ? g_i8_timeline : nullptr;\n"),
+    ("  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n",
+     "  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n"
+     "  h.tl = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n) <= size_t(g_i8_timeline_wgs)\n"
+     "             ? g_i8_timeline : nullptr;\n"),
     ("namespace i8conv {\n\n// Set by a wave of rowpass_kernel",
      "namespace i8conv {\nunsigned long long *g_i8_timeline = nullptr;\nint g_i8_timeline_wgs = 0;\n\n"
      "// Set by a wave of rowpass_kernel"),
@@ -163,6 +168,22 @@ HIPFLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+def object_flags() -> dict:
+    """Per-object HIPFLAGS additions of csrc/Makefile ("$(BUILD)/x.o ...:
+    HIPFLAGS += ..." lines), by source name: the stamped copies are built
+    with the same flags as the library's."""
+    extra = {}
+    for line in open(os.path.join(CSRC, "Makefile")).read().splitlines():
+        targets, sep, rest = line.partition(": HIPFLAGS +=")
+        if not sep:
+            continue
+        for t in targets.split():
+            if t.startswith("$(BUILD)/") and t.endswith(".o"):
+                name = t[len("$(BUILD)/"):-2] + ".hip"
+                extra[name] = extra.get(name, []) + rest.split()
+    return extra
+
+
 def build() -> str:
     """Compiles the stamped kernels and links them with the in-tree objects of
     every other source (csrc/_build, from the library's own build) into
@@ -178,8 +199,8 @@ def build() -> str:
             f.write(text)
         obj = os.path.join(BUILD, name.replace(".hip", ".o"))
         objs.append(obj)
-        procs.append(subprocess.Popen([hipcc, *HIPFLAGS, "-I", INCLUDE, "-I", CSRC, "-c", path,
-                                       "-o", obj]))
+        procs.append(subprocess.Popen([hipcc, *HIPFLAGS, *object_flags().get(name, []),
+                                       "-I", INCLUDE, "-I", CSRC, "-c", path, "-o", obj]))
     for proc in procs:
         if proc.wait() != 0:
             raise RuntimeError("timeline: compiling a stamped kernel failed")

@@ -15,7 +15,9 @@ def test_every_edit_applies_once():
     assert 'extern "C" void i8conv_timeline_set(void *buffer, int workgroups)' in \
         src["kernel_rowpass.hip"]
     for text in src.values():
-        assert "h.tl = grid <=" in text           # launches beyond the buffer stamp nothing
+        # launches beyond the buffer stamp nothing
+        assert "<= int64_t(g_i8_timeline_wgs) ? g_i8_timeline : nullptr" in text or \
+            "<= size_t(g_i8_timeline_wgs)\n             ? g_i8_timeline : nullptr" in text
         assert "tl_put(p.tl, 0, t_start);" in text
 
 
