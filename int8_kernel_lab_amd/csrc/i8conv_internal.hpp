@@ -37,6 +37,10 @@ inline int64_t deep_up_mod32(int64_t v, int64_t target) {
   const int64_t t = ((target % 32) + 32) % 32;
   return v + ((t - v % 32) + 32) % 32;
 }
+// The same on 32-bit values, for the device (|v|, |target| < 2^31).
+I8_HD constexpr int deep_up_mod32_d(int v, int target) {
+  return v + ((((target & 31) - (v & 31)) + 32) & 31);
+}
 inline int64_t deep_row_units(int64_t wp, int64_t out_w) {
   return deep_up_mod32(wp * kDeepUnits, 10 * out_w);
 }
@@ -44,6 +48,9 @@ inline int64_t deep_image_units(int64_t hp, int64_t row_units, int64_t out_h, in
   return deep_up_mod32(hp * row_units, 10 * out_h * out_w);
 }
 constexpr int kDeepMaxLoadsPerWave = 24;  // 1 KB plane loads per copy wave (<= 768 pixels)
+// Bytes of the chunk flags (filter, one per image) and the MFMA waves' halo
+// flags, in whole 256-byte blocks (the planes follow them).
+I8_HD constexpr int64_t deep_flags_bytes(int64_t n) { return ((16 * (2 + n) + 255) / 256) * 256; }
 struct DeepPlan {
   int S = 0, I = 0;       // plane row / image strides
   int loads = 0;          // 1 KB plane loads (8 input pixels each)

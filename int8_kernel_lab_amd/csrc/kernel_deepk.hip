@@ -68,23 +68,17 @@ constexpr int kDkMaxLoads = kDeepMaxLoadsPerWave;  // plane loads per copy wave
 // The source word of every flag copy.
 __device__ __attribute__((aligned(16))) int g_dk_one[4] = {1, 1, 1, 1};
 
+// The arguments past the preloaded ones (deepk_kernel).
 struct DeepArgs {
-  const int8_t *x;
-  const int8_t *w;
   int32_t *partial;
-  uint32_t x_bytes, w_bytes, partial_bytes;
-  int n, h, wd, c, pad_h, pad_w;
-  int out_w, gemm_m, gemm_n, gemm_k;
+  uint32_t partial_bytes;
+  int pad_h, pad_w;
+  int out_w, gemm_m;
   int S, I;         // plane row / image strides, 16-byte units
   int hp, wp;       // padded rows and columns per image
-  int loads;        // 1 KB plane loads (8 input pixels each)
   int frags;        // 16-pixel fragments over M
-  int tiles_n;      // 32-channel tiles
-  int per_xcd;      // grid / 8 when grid % 8 == 0, else 0 (no XCD order)
-  int flags_lds;    // LDS byte offset of the chunk flags
-  int planes_lds;   // LDS byte offset of the planes
   int spin_limit;   // polls of about 64 cycles each per bounded wait (wait_spin_limit())
-  FastDiv3 div_hw, div_w, div_hpwp, div_wp, div_ohw, div_ow;
+  FastDiv3 div_hpwp, div_wp, div_ohw, div_ow;
 };
 
 template <class F, size_t... J>
@@ -108,39 +102,87 @@ __device__ __forceinline__ void flag_wait(uint32_t addr, int spin_limit) {
   __hip_atomic_store(&g_deepk_wait_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// DeepArgs, the kernel's last argument, read from the kernel-argument
+// segment where it is called.  The segment pointer passes through an empty
+// asm first, so the compiler cannot hoist the loads to the kernel's entry:
+// there they would hold SGPRs that the copy waves' path reuses, and the copy
+// waves would wait for them (~0.3 us) before their first copy.  The
+// argument's offset: two 8-byte pointers and nine 4-byte words, rounded up
+// to the struct's 8-byte alignment.
+constexpr uint32_t kDeepArgsOffset = (2 * 8 + 9 * 4 + 7) / 8 * 8;
+static_assert(alignof(DeepArgs) == 8, "DeepArgs offset assumes 8-byte alignment");
+__device__ __forceinline__ DeepArgs deep_args() {
+  uint64_t kp = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
+  asm volatile("" : "+s"(kp));
+  const auto *src =
+      reinterpret_cast<const __attribute__((address_space(4))) uint32_t *>(kp + kDeepArgsOffset);
+  static_assert(sizeof(DeepArgs) % 4 == 0, "argument block of whole words");
+  uint32_t w[sizeof(DeepArgs) / 4];
+#pragma unroll
+  for (int i = 0; i < int(sizeof(DeepArgs) / 4); ++i) w[i] = src[i];
+  DeepArgs d;
+  __builtin_memcpy(&d, w, sizeof(d));
+  return d;
+}
+
+// The kernel's leading arguments arrive preloaded in SGPRs (this file is
+// built with -amdgpu-kernarg-preload-count=11: eleven arguments, thirteen
+// words): the input and filter base pointers, the input channels, the
+// output channels, the images, h | wd << 16, pad_h | pad_w << 8 and the
+// dividers by h*wd and wd (multiplier; add | shift << 1), which is all
+// the copy waves use: the split and channel tile of the workgroup, the
+// filter rows, the input pixels and their places in the planes.  The rest
+// of the arguments (DeepArgs, the MFMA waves' set-up) are loaded from the
+// kernel-argument segment, a cold scalar round trip of ~0.3 us after a
+// launch enqueued on a stream, while the first copies land.
 template <int NF>
-__global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) {
+__global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(
+    const int8_t *x_pre, const int8_t *w_pre, uint32_t c_pre, uint32_t gemm_n_pre,
+    uint32_t n_pre, uint32_t hw_pre, uint32_t pads_pre, uint32_t div_hw_mul,
+    uint32_t div_hw_as, uint32_t div_w_mul, uint32_t div_w_as, DeepArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-  const DeepArgs p = p_arg;
-  pin_sgprs(p);
+  (void)p_arg;  // read through deep_args() on the MFMA waves' path only
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave_id = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = int(c_pre), gemm_n = int(gemm_n_pre), n = int(n_pre);
+  const int h = int(hw_pre & 0xffffu), wd = int(hw_pre >> 16);
+  const int pad_h = int(pads_pre & 0xffu), pad_w = int(pads_pre >> 8);
+  const int gemm_k = 9 * c;
+  const int tiles_n = (gemm_n + 31) >> 5;
+  const int grid = (c >> 7) * tiles_n;
   // consecutive work items are one split's channel tiles; with the XCD
-  // order they run on one XCD and share its L2 copy of the input slice
+  // order (grids of a multiple of 8 workgroups: workgroup i runs on XCD
+  // i mod 8) they run on one XCD and share its L2 copy of the input slice
+  const int per_xcd = (grid & 7) == 0 ? grid >> 3 : 0;
   const int bid = int(blockIdx.x);
-  const int item = p.per_xcd ? (bid & 7) * p.per_xcd + (bid >> 3) : bid;
-  const int split = item / p.tiles_n;
-  const int tn = item - split * p.tiles_n;
+  const int item = per_xcd ? (bid & 7) * per_xcd + (bid >> 3) : bid;
+  const int split = int(uint32_t(item) / uint32_t(tiles_n));
+  const int tn = item - split * tiles_n;
   const uint32_t base = lds_addr(smem);
-  const uint32_t flags = base + uint32_t(p.flags_lds);
-  const int nchunks = 1 + p.n;
+  const uint32_t flags = base + uint32_t(kDkFilterBytes);
+  const int nchunks = 1 + n;
   // flags of chunk k at flags + 16 k (one word per copy wave); then the
   // MFMA waves' halo flags
   const uint32_t halo_flags = flags + 16u * uint32_t(nchunks);
+  const uint32_t planes = base + uint32_t(kDkFilterBytes + deep_flags_bytes(n));
 
   if (wave_id == 0) {
-    // every flag starts at zero before any copy can land
+    // every flag starts at zero before any flag write can land
     for (int k = lane; k <= nchunks; k += 64)
       asm volatile("ds_write_b128 %0, %1" ::"v"(flags + 16u * uint32_t(k)), "v"(v4i{0, 0, 0, 0})
                    : "memory");
   }
-  __syncthreads();
+  // The workgroup barrier orders wave 0's flag writes before every flag
+  // write and flag read; it waits for LDS operations only.  The copy waves
+  // pass it once their filter copies are issued: those may land at any
+  // time, the flags only after it.
+  auto barrier = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
   if (wave_id >= 4) {
     const int cw = wave_id - 4;
-    const v4u wd = make_desc(p.w, p.w_bytes);
+    const v4u wdesc = make_desc(w_pre, uint32_t(gemm_n) * uint32_t(gemm_k));
     const v4u one = make_desc(g_dk_one, 16u);
     auto signal = [&](int k) {
       if (lane == 0) lds_copy4(one, flags + 16u * uint32_t(k) + 4u * uint32_t(cw), 0u);
@@ -158,11 +200,13 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
       const int row = 8 * half + frow;
       const int oc = tn * 32 + 16 * a + row;
       const uint32_t off =
-          oc < p.gemm_n ? uint32_t(oc) * uint32_t(p.gemm_k) +
-                              uint32_t(t * p.c + split * 128 + 16 * swz128_chunk(row, fchunk0))
-                        : kOutOfRange;
-      lds_copy16(wd, base + uint32_t(blk * 2048 + half * 1024), off);
+          oc < gemm_n ? uint32_t(oc) * uint32_t(gemm_k) +
+                            uint32_t(t * c + split * 128 + 16 * swz128_chunk(row, fchunk0))
+                      : kOutOfRange;
+      lds_copy16(wdesc, base + uint32_t(blk * 2048 + half * 1024), off);
     }
+    // the filter's flag right behind it: a wave's loads land in issue order
+    barrier();
     signal(0);
     // chunks 1..n, the planes: load i (8 input pixels, lane -> pixel
     // 8 i + lane / 8, 16-byte unit lane % 8: whole 128-byte lines) goes
@@ -171,13 +215,19 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
     // and sets its flag of chunk k once it has written every one of its
     // loads that holds a pixel of image k - 1 (LDS writes of a wave land in
     // order, so the flag lands after them)
-    const uint32_t planes = base + uint32_t(p.planes_lds);
     const uint32_t col0 = uint32_t(split * 128);
-    const int npix = p.n * p.h * p.wd;
-    const int hw = p.h * p.wd;
-    const auto xr = make_rsrc(p.x, p.x_bytes);
-    const int nload = p.loads > cw ? (p.loads - cw + 3) / 4 : 0;  // <= kDkMaxLoads
+    const int hw = h * wd;
+    const int npix = n * hw;
+    const auto xr = make_rsrc(x_pre, uint32_t(npix) * uint32_t(c));
+    const int loads = (npix + 7) >> 3;
+    const int nload = loads > cw ? (loads - cw + 3) / 4 : 0;  // <= kDkMaxLoads
     const int u = lane & 7;
+    const FastDiv3 div_hw{div_hw_mul, div_hw_as & 1u, div_hw_as >> 1};
+    const FastDiv3 div_w{div_w_mul, div_w_as & 1u, div_w_as >> 1};
+    // plane strides (deep_row_units, deep_image_units)
+    const int out_h = h + 2 * pad_h - 2, out_w = wd + 2 * pad_w - 2;
+    const int S = deep_up_mod32_d((wd + 2 * pad_w) * kDkUnits, 10 * out_w);
+    const int I = deep_up_mod32_d((h + 2 * pad_h) * S, 10 * out_h * out_w);
     // Exactly kDkMaxLoads loads per wave, those past the wave's share out of
     // range (no memory access): the wait for load j is then the constant
     // vmcnt(kDkMaxLoads - 1 - j).  (A run-time vmcnt needs a switch per wait;
@@ -187,7 +237,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
     for (int j = 0; j < kDkMaxLoads; ++j) {
       const int pix = 8 * (cw + 4 * j) + (lane >> 3);
       data[j] = load16(xr, j < nload && pix < npix
-                               ? uint32_t(pix) * uint32_t(p.c) + col0 + 16u * uint32_t(u)
+                               ? uint32_t(pix) * uint32_t(c) + col0 + 16u * uint32_t(u)
                                : kOutOfRange);
     }
     auto signal_ds = [&](int k) {
@@ -199,44 +249,48 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
     // last load holding a pixel of image k - 1
     auto last_load = [&](int k) { return (k * hw - 1) >> 3; };
     int kdone = 1;
-    while (kdone <= p.n && last_load(kdone) < cw) signal_ds(kdone++);
+    while (kdone <= n && last_load(kdone) < cw) signal_ds(kdone++);
     auto step = [&](auto jc) {
       constexpr int j = decltype(jc)::value;
       if (j >= nload) return;
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDkMaxLoads - 1 - j) : "memory");
       const int pix = 8 * (cw + 4 * j) + (lane >> 3);
       if (pix < npix) {
-        const int b = int(fast_div(uint32_t(pix), p.div_hw));
+        const int b = int(fast_div(uint32_t(pix), div_hw));
         const int rem = pix - b * hw;
-        const int iy = int(fast_div(uint32_t(rem), p.div_w));
-        const int ix = rem - iy * p.wd;
+        const int iy = int(fast_div(uint32_t(rem), div_w));
+        const int ix = rem - iy * wd;
         const uint32_t unit =
-            uint32_t(b * p.I + (iy + p.pad_h) * p.S + (ix + p.pad_w) * kDkUnits + u);
+            uint32_t(b * I + (iy + pad_h) * S + (ix + pad_w) * kDkUnits + u);
         *reinterpret_cast<__attribute__((address_space(3))) v4i *>(size_t(planes + 16u * unit)) =
             data[j];
       }
       const int next = cw + 4 * (j + 1);
-      while (kdone <= p.n && last_load(kdone) < next) signal_ds(kdone++);
+      while (kdone <= n && last_load(kdone) < next) signal_ds(kdone++);
     };
     for_each_index(step, std::make_index_sequence<kDkMaxLoads>{});
-    while (kdone <= p.n) signal_ds(kdone++);
+    while (kdone <= n) signal_ds(kdone++);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     return;
   }
 
+  // the remaining arguments, in one batch, after the barrier (which then
+  // waits for wave 0's flag writes only)
+  barrier();
+  const DeepArgs p = deep_args();
+  pin_sgprs(p);
   // MFMA wave: zero the halo pixels of the planes (the padding rows and
   // columns every tap may read; units 0..7), a quarter each, then flag it
   const int wv = wave_id;
-  const uint32_t planes = base + uint32_t(p.planes_lds);
   {
     const int hpwp = p.hp * p.wp;
-    for (int j = lane + 64 * wv; j < p.n * hpwp; j += 256) {
+    for (int j = lane + 64 * wv; j < n * hpwp; j += 256) {
       const int b = int(fast_div(uint32_t(j), p.div_hpwp));
       const int r = j - b * hpwp;
       const int prow = int(fast_div(uint32_t(r), p.div_wp));
       const int pcol = r - prow * p.wp;
-      const bool inside = unsigned(prow - p.pad_h) < unsigned(p.h) &&
-                          unsigned(pcol - p.pad_w) < unsigned(p.wd);
+      const bool inside = unsigned(prow - p.pad_h) < unsigned(h) &&
+                          unsigned(pcol - p.pad_w) < unsigned(wd);
       if (!inside) {
         auto *z = reinterpret_cast<__attribute__((address_space(3))) v4i *>(
             size_t(planes + 16u * uint32_t(b * p.I + prow * p.S + pcol * kDkUnits)));
@@ -263,7 +317,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
             smem + (t * 2 + a) * 2048 + swz128(lane & 15, 4 * hk + (lane >> 4)));
 
   const auto pr = make_rsrc(p.partial, p.partial_bytes);
-  const int ohw = p.gemm_m / p.n;
+  const int ohw = p.gemm_m / n;
   // B fragment base address of fragment f for this lane; lanes past the
   // last pixel read the last pixel again (never stored)
   auto frag_addr = [&](int f) {
@@ -295,10 +349,10 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
     const v4i da = lo ? acc0 : r, db = lo ? r : acc0;
     const int ma = 16 * f + (lo ? px : px - 8), mb = 16 * f + (lo ? px + 8 : px);
     const int oca = tn * 32 + (lo ? 4 * g : 16 + 4 * g), ocb = tn * 32 + (lo ? 16 + 4 * g : 4 * g);
-    if (ma < p.gemm_m && oca < p.gemm_n)
-      store_out4<kStoreThrough>(pr, ((sbase + uint32_t(ma)) * uint32_t(p.gemm_n) + uint32_t(oca)) * 4u, da);
-    if (mb < p.gemm_m && ocb < p.gemm_n)
-      store_out4<kStoreThrough>(pr, ((sbase + uint32_t(mb)) * uint32_t(p.gemm_n) + uint32_t(ocb)) * 4u, db);
+    if (ma < p.gemm_m && oca < gemm_n)
+      store_out4<kStoreThrough>(pr, ((sbase + uint32_t(ma)) * uint32_t(gemm_n) + uint32_t(oca)) * 4u, da);
+    if (mb < p.gemm_m && ocb < gemm_n)
+      store_out4<kStoreThrough>(pr, ((sbase + uint32_t(mb)) * uint32_t(gemm_n) + uint32_t(ocb)) * 4u, db);
   };
   // One fragment at a time, four accumulator chains (channel fragment a x
   // k-half hk), B fragments two taps ahead of the MFMAs that use them; the
@@ -350,8 +404,9 @@ __global__ __launch_bounds__(2 * kThreads, 1) void deepk_kernel(DeepArgs p_arg) 
 
 bool plan_deepk(const i8conv_shape &s, const i8conv_geometry &g, DeepPlan *out) {
   if (s.r != 3 || s.s != 3 || s.stride_h != 1 || s.stride_w != 1 || s.dilation_h != 1 ||
-      s.dilation_w != 1 || s.c % 128 != 0 || s.c < 256 || g.gemm_n % 4 != 0)
-    return false;
+      s.dilation_w != 1 || s.c % 128 != 0 || s.c < 256 || g.gemm_n % 4 != 0 ||
+      s.h >= 65536 || s.w >= 65536 || s.pad_h >= 256 || s.pad_w >= 256)
+    return false;  // (h | w << 16 and pad_h | pad_w << 8 are preloaded argument words)
   const int64_t hp = int64_t(s.h) + 2 * s.pad_h, wp = int64_t(s.w) + 2 * s.pad_w;
   if (g.out_h != hp - 2 || g.out_w != wp - 2 || g.out_h < 1 || g.out_w < 1) return false;
   const int64_t frags = (g.gemm_m + 15) / 16;
@@ -363,7 +418,7 @@ bool plan_deepk(const i8conv_shape &s, const i8conv_geometry &g, DeepPlan *out) 
   const int64_t loads = (int64_t(s.n) * s.h * s.w + 7) / 8;
   if ((loads + 3) / 4 > kDkMaxLoads) return false;
   // chunk flags (filter, one per image) and the MFMA waves' halo flags
-  const int64_t flags_bytes = ((16 * (2 + int64_t(s.n)) + 255) / 256) * 256;
+  const int64_t flags_bytes = deep_flags_bytes(s.n);
   const int64_t lds = kDkFilterBytes + flags_bytes + units * 16;
   if (lds > kLdsBudget) return false;
   const int64_t splits = s.c / 128, tiles_n = (g.gemm_n + 31) / 32;
@@ -384,37 +439,31 @@ bool plan_deepk(const i8conv_shape &s, const i8conv_geometry &g, DeepPlan *out) 
 }
 
 int launch_deepk(const ConvArgs &a, const DeepPlan &p, void *workspace, void *stream) {
+  const FastDiv3 div_hw = make_fastdiv3(uint32_t(a.h * a.wd));
+  const FastDiv3 div_w = make_fastdiv3(uint32_t(a.wd));
+  if (a.h >= 65536 || a.wd >= 65536 || a.c % 128 != 0 || a.pad_h < 0 || a.pad_h >= 256 ||
+      a.pad_w < 0 || a.pad_w >= 256 || p.S != deep_up_mod32_d((a.wd + 2 * a.pad_w) * kDkUnits, 10 * a.out_w) ||
+      p.I != deep_up_mod32_d((a.h + 2 * a.pad_h) * p.S, 10 * a.out_h * a.out_w) ||
+      int64_t(a.c / 128) * ((a.gemm_n + 31) / 32) != int64_t(p.splits) * p.tiles_n ||
+      p.planes_lds != kDkFilterBytes + deep_flags_bytes(a.n) ||
+      (int64_t(a.n) * a.h * a.wd + 7) / 8 != p.loads) {
+    set_error("deep-channel split-K: plan and shape disagree");
+    return I8CONV_BAD_ARGUMENT;
+  }
   DeepArgs h{};
-  h.x = a.x;
-  h.w = a.w;
   h.partial = static_cast<int32_t *>(workspace);
   h.spin_limit = wait_spin_limit();
-  h.x_bytes = a.x_bytes;
-  h.w_bytes = a.w_bytes;
   h.partial_bytes = uint32_t(int64_t(p.splits) * a.gemm_m * a.gemm_n * 4);
-  h.n = a.n;
-  h.h = a.h;
-  h.wd = a.wd;
-  h.c = a.c;
   h.pad_h = a.pad_h;
   h.pad_w = a.pad_w;
   h.out_w = a.out_w;
   h.gemm_m = a.gemm_m;
-  h.gemm_n = a.gemm_n;
-  h.gemm_k = a.gemm_k;
   h.S = p.S;
   h.I = p.I;
   h.hp = a.h + 2 * a.pad_h;
   h.wp = a.wd + 2 * a.pad_w;
-  h.loads = p.loads;
   h.frags = p.frags;
-  h.tiles_n = p.tiles_n;
   const int64_t grid = int64_t(p.splits) * p.tiles_n;
-  h.per_xcd = grid % 8 == 0 ? int(grid / 8) : 0;
-  h.flags_lds = p.flags_lds;
-  h.planes_lds = p.planes_lds;
-  h.div_hw = make_fastdiv3(uint32_t(a.h * a.wd));
-  h.div_w = make_fastdiv3(uint32_t(a.wd));
   h.div_hpwp = make_fastdiv3(uint32_t(h.hp * h.wp));
   h.div_wp = make_fastdiv3(uint32_t(h.wp));
   h.div_ohw = make_fastdiv3(uint32_t(a.out_h * a.out_w));
@@ -430,7 +479,11 @@ int launch_deepk(const ConvArgs &a, const DeepPlan &p, void *workspace, void *st
         return I8CONV_HIP_ERROR;
       }
     }
-    hipLaunchKernelGGL(kern, dim3(unsigned(grid)), dim3(2 * kThreads), p.lds, s, h);
+    hipLaunchKernelGGL(kern, dim3(unsigned(grid)), dim3(2 * kThreads), p.lds, s, a.x, a.w,
+                       uint32_t(a.c), uint32_t(a.gemm_n), uint32_t(a.n),
+                       uint32_t(a.h) | uint32_t(a.wd) << 16,
+                       uint32_t(a.pad_h) | uint32_t(a.pad_w) << 8, div_hw.mul,
+                       div_hw.add | div_hw.shift << 1, div_w.mul, div_w.add | div_w.shift << 1, h);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
       set_error(std::string("deep-channel split-K launch: ") + hipGetErrorString(e));

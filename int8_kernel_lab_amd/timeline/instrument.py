@@ -31,7 +31,7 @@ ROWPASS_SLOTS = {0: "wave start", 1: "MFMA wave: arguments loaded", 31: "past th
 ROWPASS_SLOTS.update({4 + r: f"MFMA wave: input row {r} ready" for r in range(10)})
 ROWPASS_CYCLES = (26, 28)  # s_memtime at walk start / end (shader clock cycles)
 # Deep-channel split-K: slot -> meaning
-DEEPK_SLOTS = {0: "wave start", 1: "arguments loaded", 3: "copy wave: plane loads issued",
+DEEPK_SLOTS = {0: "wave start", 1: "MFMA wave: arguments loaded", 3: "copy wave: plane loads issued",
                20: "copy wave: planes written", 21: "MFMA wave: halo zeroed",
                23: "MFMA wave: filter landed", 24: "MFMA wave: stores drained"}
 DEEPK_SLOTS.update({4 + k: f"copy wave: image {k} flagged" for k in range(16)})
@@ -106,12 +106,18 @@ DEEPK_EDITS = [
      "  int spin_limit;   // polls of about 64 cycles each per bounded wait (wait_spin_limit())\n"
      "  unsigned long long *tl;"),
     ("__device__ __forceinline__ bool flags_set(v4i f) {", _STAMP + "__device__ __forceinline__ bool flags_set(v4i f) {"),
-    ("  const DeepArgs p = p_arg;\n  pin_sgprs(p);\n",
-     "  const unsigned long long t_start = tl_now();\n  const DeepArgs p = p_arg;\n  pin_sgprs(p);\n"
+    ("  (void)p_arg;  // read through deep_args() on the MFMA waves' path only\n",
+     "  const unsigned long long t_start = tl_now();\n  (void)p_arg;\n"),
+    ("  const DeepArgs p = deep_args();\n  pin_sgprs(p);\n",
+     "  const DeepArgs p = deep_args();\n  pin_sgprs(p);\n"
      "  tl_put(p.tl, 0, t_start);\n  tl_put(p.tl, 1, tl_now());\n"),
-    ("    auto signal_ds = [&](int k) {\n      if (lane == 0)",
-     "    tl_put(p.tl, 3, tl_now());\n    auto signal_ds = [&](int k) {\n"
-     "      tl_put(p.tl, 4 + (k - 1) % 16, tl_now());\n      if (lane == 0)"),
+    ("                               : kOutOfRange);\n    }\n    auto signal_ds = [&](int k) {\n",
+     "                               : kOutOfRange);\n    }\n    const DeepArgs p = deep_args();\n"
+     "    tl_put(p.tl, 0, t_start);\n    tl_put(p.tl, 3, tl_now());\n"
+     "    auto signal_ds = [&](int k) {\n"),
+    ("    auto signal_ds = [&](int k) {\n      if (lane == 0)\n        asm volatile(\"ds_write_b32",
+     "    auto signal_ds = [&](int k) {\n"
+     "      tl_put(p.tl, 4 + (k - 1) % 16, tl_now());\n      if (lane == 0)\n        asm volatile(\"ds_write_b32"),
     ("    asm volatile(\"s_waitcnt vmcnt(0) lgkmcnt(0)\" ::: \"memory\");\n    return;",
      "    asm volatile(\"s_waitcnt vmcnt(0) lgkmcnt(0)\" ::: \"memory\");\n"
      "    tl_put(p.tl, 20, tl_now());\n    return;"),
