@@ -37,27 +37,75 @@
 namespace i8conv {
 namespace {
 
-// Everything the kernel reads; loaded into SGPRs in one batch.
+// The arguments of the walk and the stores (the copies' come preloaded:
+// see row_kernel).
 struct RowArgs {
-  const int8_t *x;
-  const int8_t *w;
-  const int32_t *bias;
   int32_t *y;
-  uint32_t x_bytes, w_bytes;
-  int n, h, wd, c, pad_h, pad_w;
-  int out_h, out_w, gemm_n, gemm_k;
-  int hp;           // padded rows per image: h + 2*pad_h
-  int wp;           // padded columns: w + 2*pad_w (== out_w + 2)
-  int pitch;        // LDS bytes per input pixel: c + 32
-  int units;        // 16-byte units per pixel in LDS: c / 16 + 2
-  int row_copies;   // 1 KB copies per padded input row
+  int n, out_h, out_w, gemm_n;
   int row_bytes;    // LDS bytes between consecutive rows
-  int input_bytes;  // LDS bytes of the input rows
-  int blocks;       // output-row blocks per image
-  int ring;         // filter staging slots in LDS
-  int tiles_n;
-  FastDiv div_hp, div_units, div_row_copies, div_blocks, div_tiles_n;
 };
+
+// RowArgs, the kernel's last argument, read from the kernel-argument segment
+// where it is called.  The segment pointer passes through an empty asm, so
+// the compiler cannot hoist the loads to the kernel's entry, where they would
+// hold SGPRs that the copy code reuses and make it wait for them (~0.3 us)
+// before its first copy.  The offset: three 8-byte pointers and five 4-byte
+// words, rounded up to the struct's 8-byte alignment.
+constexpr uint32_t kRowArgsOffset = (3 * 8 + 5 * 4 + 7) / 8 * 8;
+static_assert(alignof(RowArgs) == 8, "RowArgs offset assumes 8-byte alignment");
+__device__ __forceinline__ RowArgs row_args() {
+  uint64_t kp = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
+  asm volatile("" : "+s"(kp));
+  const auto *src =
+      reinterpret_cast<const __attribute__((address_space(4))) uint32_t *>(kp + kRowArgsOffset);
+  static_assert(sizeof(RowArgs) % 4 == 0, "argument block of whole words");
+  uint32_t w[sizeof(RowArgs) / 4];
+#pragma unroll
+  for (int i = 0; i < int(sizeof(RowArgs) / 4); ++i) w[i] = src[i];
+  RowArgs r;
+  __builtin_memcpy(&r, w, sizeof(r));
+  return r;
+}
+
+// Padded input rows vr0 .. vr0 + nrows - 1 (image-major: row hp of image b
+// is row 0 of image b + 1) into LDS, 1 KB LDS-DMA copies dealt round-robin
+// to the four waves, as copy_input_rows (halo_common.hpp) but with the
+// pixel's 16-byte units a compile-time count (c = 64 CG) and no run-time
+// dividers: a wave's copies q = wave, wave + 4, ... walk the (row, copy)
+// pairs in order, and a row past the image's last (vr0's image b, at most
+// hp rows later) is the next image's.
+template <int CG>
+__device__ __forceinline__ void copy_rows_pre(v4u xd, uint32_t lds0, int b, int oy0, int nrows,
+                                              int wave, int lane, int row_copies, int row_bytes,
+                                              int hp, int n, int h, int wd, int pad_h,
+                                              int pad_w) {
+  constexpr int kC = 64 * CG;
+  constexpr int kUnits = kC / 16 + kRowPadUnits;
+  int rr = 0, j = wave;
+  while (j >= row_copies) {
+    j -= row_copies;
+    ++rr;
+  }
+  for (; rr < nrows;) {
+    const int pr = oy0 + rr;
+    const int bb = b + (pr >= hp ? 1 : 0);
+    const int iy = pr - (pr >= hp ? hp : 0) - pad_h;
+    const bool row_ok = bb < n && unsigned(iy) < unsigned(h);
+    // modulo 2^32: exact wherever it is used (the sum below is in [0, 2^31))
+    const uint32_t row_off = uint32_t((bb * h + iy) * wd - pad_w) * uint32_t(kC);
+    const int slot = j * 64 + lane;
+    const int pix = slot / kUnits;
+    const int u = slot - pix * kUnits;
+    const bool ok = row_ok && u < (kC >> 4) && unsigned(pix - pad_w) < unsigned(wd);
+    const uint32_t off = ok ? row_off + uint32_t(pix * kC + 16 * u) : kOutOfRange;
+    lds_copy16(xd, lds0 + rr * row_bytes + j * 1024, off);
+    j += 4;
+    while (j >= row_copies) {
+      j -= row_copies;
+      ++rr;
+    }
+  }
+}
 
 template <int FN, int CG, int NFR>
 struct RowState {
@@ -178,56 +226,81 @@ __device__ __forceinline__ void take_chunks(FilterRing<FN, 9 * CG> &ring,
 
 // kPolicy: the output store policy, write-through where the pixel pitch is
 // sector-aligned (sector_pitch), else ordinary.
+// The leading arguments arrive preloaded in SGPRs (this file is built with
+// -amdgpu-kernarg-preload-count=8: eight arguments, eleven words): the
+// input, filter and bias pointers, the images, h | wd << 16, pad_h | pad_w
+// << 8 | blocks << 16 (row blocks per image), the output channels and ring |
+// rows << 8 (filter ring slots, LDS input rows), from which every copy is
+// derived; RowArgs follows for the walk.  The grid is (channel tiles, row
+// blocks, images).
 template <int FN, int CG, int NFR, int kPolicy>
-__global__ __launch_bounds__(kThreads, 1) void row_kernel(RowArgs p_arg) {
+__global__ __launch_bounds__(kThreads, 1) void row_kernel(
+    const int8_t *x_pre, const int8_t *w_pre, const int32_t *bias_pre, uint32_t n_pre,
+    uint32_t hw_pre, uint32_t pads_pre, uint32_t gemm_n_pre, uint32_t ring_pre, RowArgs p_arg) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-  const RowArgs p = p_arg;
-  pin_sgprs(p);
+  (void)p_arg;  // read through row_args() once the copies are issued
   constexpr int kSteps = 9 * CG;
   constexpr int kChunks = (kSteps + 1) / 2;
+  constexpr int kC = 64 * CG;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int rest = int(fast_div(blockIdx.x, p.div_tiles_n));
-  const int tn = int(blockIdx.x) - rest * p.tiles_n;
-  const int b = int(fast_div(uint32_t(rest), p.div_blocks));
-  const int q = rest - b * p.blocks;
-  const int oy0 = int((int64_t(q) * p.out_h) / p.blocks);
-  const int rows_out = int((int64_t(q + 1) * p.out_h) / p.blocks) - oy0;
+  const int n = int(n_pre);
+  const int h = int(hw_pre & 0xffffu), wd = int(hw_pre >> 16);
+  const int pad_h = int(pads_pre & 0xffu), pad_w = int((pads_pre >> 8) & 0xffu);
+  const int blocks = int(pads_pre >> 16);
+  const int gemm_n = int(gemm_n_pre);
+  const int ring_slots = int(ring_pre & 0xffu), rows_lds = int(ring_pre >> 8);
+  const int hp = h + 2 * pad_h, wp = wd + 2 * pad_w;
+  const int out_h = hp - 2;
+  // the LDS row layout (halo_row_layout with kRowPadUnits)
+  constexpr int kUnits = kC / 16 + kRowPadUnits;
+  const int row_units = wp * kUnits;
+  const int row_copies = (row_units + 63) >> 6;
+  const int row_bytes = 16 * (64 * row_copies + (((row_units - 64 * row_copies) % 16) + 16) % 16);
+
+  const int tn = int(blockIdx.x);
+  const int q = int(blockIdx.y);
+  const int b = int(blockIdx.z);
+  // out_h < 2^16 and q < blocks <= out_h: the products fit in 32 bits
+  const int oy0 = int(uint32_t(q * out_h) / uint32_t(blocks));
+  const int rows_out = int(uint32_t((q + 1) * out_h) / uint32_t(blocks)) - oy0;
   const int tile_n = tn * 64 * FN;
 
   const int8_t *bias_lds = smem + wave * 256;
-  stage_bias<FN>(p.bias, p.gemm_n, tile_n + wave * 16 * FN, bias_lds, lane);
+  stage_bias<FN>(bias_pre, gemm_n, tile_n + wave * 16 * FN, bias_lds, lane);
 
   // padded input rows oy0 .. oy0 + rows_out + 1 of image b
   const int8_t *rows = smem + kHaloBiasLds;
-  copy_input_rows(make_desc(p.x, p.x_bytes), lds_addr(rows), b * p.hp + oy0, rows_out + 2, wave,
-                  lane, p.row_copies, p.div_row_copies, p.row_bytes, p.div_hp, p.hp, p.units,
-                  p.div_units, p.n, p.h, p.wd, p.c, p.pad_h, p.pad_w);
+  copy_rows_pre<CG>(make_desc(x_pre, uint32_t(n) * uint32_t(h) * uint32_t(wd) * uint32_t(kC)),
+                    lds_addr(rows), b, oy0, rows_out + 2, wave, lane, row_copies, row_bytes, hp,
+                    n, h, wd, pad_h, pad_w);
 
   FilterRing<FN, kSteps> ring;
-  ring.wd = make_desc(p.w, p.w_bytes);
-  ring.ptr = rows + p.input_bytes;
+  ring.wd = make_desc(w_pre, uint32_t(gemm_n) * uint32_t(9 * kC));
+  ring.ptr = rows + rows_lds * row_bytes;
   ring.lds = lds_addr(ring.ptr);
-  ring.slots = p.ring;
+  ring.slots = ring_slots;
   ring.cur = 0;
   ring.wave = wave;
   ring.lane = lane;
-  ring.init(tile_n, p.gemm_n, p.gemm_k);
+  ring.init(tile_n, gemm_n, 9 * kC);
   for (int c = 0; c < ring.slots && c < kChunks; ++c) ring.issue(c, c);
 
+  const RowArgs p = row_args();
+  pin_sgprs(p);
   RowState<FN, CG, NFR> st;
 #pragma unroll
   for (int fx = 0; fx < 3; ++fx)
 #pragma unroll
     for (int j = 0; j < NFR; ++j) {
       // columns past the padded row (read only for dropped lanes) are clamped
-      const int col = min(16 * j + (lane & 15) + fx, p.wp - 1);
-      st.colofs[fx][j] = col * p.pitch + 16 * (lane >> 4);
+      const int col = min(16 * j + (lane & 15) + fx, wp - 1);
+      st.colofs[fx][j] = col * (kC + 16 * kRowPadUnits) + 16 * (lane >> 4);
     }
-  const int m_row0 = (b * p.out_h + oy0) * p.out_w;
+  const int m_row0 = (b * out_h + oy0) * p.out_w;
 
   // Input row ir feeds output rows ir - fy (fy = 0, 1, 2) that exist:
   // row 0 only fy = 0, row 1 fy <= 1, rows 2 .. rows_out - 1 all three, row
@@ -286,8 +359,16 @@ __global__ __launch_bounds__(kThreads, 1) void row_kernel(RowArgs p_arg) {
 #undef I8_ROW
 }
 
+// The preloaded leading arguments of row_kernel.
+struct RowPre {
+  const int8_t *x;
+  const int8_t *w;
+  const int32_t *bias;
+  uint32_t n, hw, pads, gemm_n, ring;
+};
+
 template <int FN, int CG, int NFR>
-int launch_t(const RowArgs &h, size_t blocks, size_t lds, hipStream_t s) {
+int launch_t(const RowPre &a, const RowArgs &h, dim3 grid, size_t lds, hipStream_t s) {
   auto kern = (h.gemm_n & 7) == 0 ? row_kernel<FN, CG, NFR, kStoreThrough>
                                   : row_kernel<FN, CG, NFR, 0>;
   if (lds > 64 * 1024) {
@@ -299,7 +380,8 @@ int launch_t(const RowArgs &h, size_t blocks, size_t lds, hipStream_t s) {
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(kThreads), lds, s, h);
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, a.x, a.w, a.bias, a.n, a.hw, a.pads,
+                     a.gemm_n, a.ring, h);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error(std::string("row kernel launch: ") + hipGetErrorString(e));
@@ -332,42 +414,32 @@ int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream) {
     set_error("row plan out of range");
     return I8CONV_BAD_ARGUMENT;
   }
+  if (a.h >= 65536 || a.wd >= 65536 || a.pad_h < 0 || a.pad_h >= 256 || a.pad_w < 0 ||
+      a.pad_w >= 256 || p.ranges >= 65536 || a.n >= 65536 || p.ring >= 256 ||
+      int64_t(p.rows) >= (int64_t(1) << 24) || a.out_h != a.h + 2 * a.pad_h - 2) {
+    set_error("row plan: geometry beyond the packed kernel arguments");
+    return I8CONV_BAD_ARGUMENT;
+  }
+  RowPre pre;
+  pre.x = a.x;
+  pre.w = a.w;
+  pre.bias = a.bias;
+  pre.n = uint32_t(a.n);
+  pre.hw = uint32_t(a.h) | uint32_t(a.wd) << 16;
+  pre.pads = uint32_t(a.pad_h) | uint32_t(a.pad_w) << 8 | uint32_t(p.ranges) << 16;
+  pre.gemm_n = uint32_t(a.gemm_n);
+  pre.ring = uint32_t(p.ring) | uint32_t(p.rows) << 8;
   RowArgs h{};
-  h.x = a.x;
-  h.w = a.w;
-  h.bias = a.bias;
   h.y = a.y;
-  h.x_bytes = a.x_bytes;
-  h.w_bytes = a.w_bytes;
   h.n = a.n;
-  h.h = a.h;
-  h.wd = a.wd;
-  h.c = a.c;
-  h.pad_h = a.pad_h;
-  h.pad_w = a.pad_w;
   h.out_h = a.out_h;
   h.out_w = a.out_w;
   h.gemm_n = a.gemm_n;
-  h.gemm_k = a.gemm_k;
-  h.hp = a.h + 2 * a.pad_h;
-  h.wp = a.wd + 2 * a.pad_w;
-  h.pitch = a.c + 16 * kRowPadUnits;
-  h.units = int(row.units);
-  h.row_copies = int(row.row_copies);
   h.row_bytes = int(row.row_bytes);
-  h.input_bytes = p.rows * h.row_bytes;
-  h.blocks = p.ranges;
-  h.ring = p.ring;
-  h.tiles_n = p.tiles_n;
-  h.div_hp = make_fastdiv(uint32_t(h.hp));
-  h.div_units = make_fastdiv(uint32_t(h.units));
-  h.div_row_copies = make_fastdiv(uint32_t(h.row_copies));
-  h.div_blocks = make_fastdiv(uint32_t(h.blocks));
-  h.div_tiles_n = make_fastdiv(uint32_t(h.tiles_n));
-  const size_t grid = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n);
+  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define I8_ROW_CASE(FN, CG, NFR) \
-  if (fn == FN && cg == CG && nfr == NFR) return launch_t<FN, CG, NFR>(h, grid, lds, s);
+  if (fn == FN && cg == CG && nfr == NFR) return launch_t<FN, CG, NFR>(pre, h, grid, lds, s);
   I8_ROW_CASE(2, 1, 1) I8_ROW_CASE(2, 1, 2) I8_ROW_CASE(2, 2, 1) I8_ROW_CASE(2, 2, 2)
   I8_ROW_CASE(1, 1, 1) I8_ROW_CASE(1, 1, 2) I8_ROW_CASE(1, 1, 3) I8_ROW_CASE(1, 1, 4)
   I8_ROW_CASE(1, 2, 1) I8_ROW_CASE(1, 2, 2) I8_ROW_CASE(1, 2, 3) I8_ROW_CASE(1, 2, 4)

@@ -298,6 +298,10 @@ bool plan_row(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
   if (!(s.r == 3 && s.s == 3 && s.stride_h == 1 && s.stride_w == 1 && s.dilation_h == 1 &&
         s.dilation_w == 1 && s.c % 64 == 0))
     return false;
+  // the row kernels' geometry travels in packed preloaded argument words and
+  // their grid is (channel tiles, row blocks, images)
+  if (s.n >= 65536 || s.h >= 65536 || s.w >= 65536 || s.pad_h >= 256 || s.pad_w >= 256)
+    return false;
   const int cg = s.c / 64;
   const int nfr = int(ceil_div(g.out_w, 16));
   const HaloRowLayout row = halo_row_layout(int64_t(s.w) + 2 * s.pad_w, s.c, kRowPadUnits);
@@ -344,10 +348,7 @@ bool plan_row(const i8conv_shape &s, const i8conv_geometry &g, PatchPlan *p) {
   if (found && s.c == 128 && p->bn == 64 && rowpass_nfr(g.out_w) != 0 &&
       p->rows - 2 <= rowpass_max_rows(rowpass_nfr(g.out_w)) &&
       rowpass_lds_bytes(s.w + 2 * s.pad_w, p->rows - 2) <= size_t(kLdsBudget) &&
-      g.output_elements * 4 <= INT32_MAX &&
-      // its geometry travels in packed preloaded argument words, its grid
-      // is (channel tiles, row blocks, images)
-      s.n < 65536 && s.h < 65536 && s.w < 65536 && s.pad_h < 256 && s.pad_w < 256)
+      g.output_elements * 4 <= INT32_MAX)
     p->streamed = true;
   return found;
 }
