@@ -727,6 +727,10 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(
   }
   // the remaining arguments, in one batch, while the first chunk lands
   pin_sgprs(p);
+  // The MFMA waves issue ahead of the copy waves that share their SIMDs
+  // (wave priority, not stream priority): 28x28x128, 5.47-5.48 -> 5.38-5.43
+  // us per launch at K = 20, same box.
+  __builtin_amdgcn_s_setprio(3);
   flag_barrier();
   run_walk<R, NFR, NG, kQ, 0, (kSplit > 0 ? kSplit : R)>(p, smem, wave, lane, b, oy0, rows_out,
                                                           tile_n, qm, qs);
