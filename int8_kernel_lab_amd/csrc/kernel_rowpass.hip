@@ -554,17 +554,12 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
     walks(std::integral_constant<int, kStoreElem>{});
 }
 
-// Output rows the MFMA waves walk when the copy waves take the rest of the
-// block once their copies have landed (0: the MFMA waves walk all R rows).
-// The copy waves are free from about the time the last input row lands, so
-// they take the block's last rows; the MFMA waves, which start after the
-// first chunk, take the first (R + 2) / 2.  Only the requantizing instances
-// split: their epilogue's VALU work per value is what a second walking wave
-// per SIMD hides (28x28x128, int8 output: 8.97 -> 8.39 us per launch); with
-// int32 output the split measured 6.47-6.49 against 6.50-6.61 us, no gain.
-constexpr int split_rows(int R, int NG, bool kQ) {
-  return kQ && NG == 2 && R >= 4 ? (R + 2) / 2 : 0;
-}
+// The MFMA waves walk every output row of the block.  (The requantizing
+// instances once let the copy waves walk the block's last rows once their
+// copies had landed, so that a second wave per SIMD shared the epilogue's
+// VALU work: 8.97 -> 8.39 us per launch on 28x28x128 with int8 output; with
+// the kernel arguments preloaded it measured 7.64-8.04 against 6.92-7.09 us
+// without, same box, and was removed.)
 
 // The kernel's leading arguments arrive preloaded in SGPRs (this file is
 // built with -amdgpu-kernarg-preload-count=7: seven arguments, ten words):
@@ -620,18 +615,16 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(
   const int8_t *halves = ring + wave * kHalves * 1024;
   const uint32_t flags = lds_addr(ring) + uint32_t(4 * kHalves * 1024);
   constexpr int nchunks = (kGroups / NG) * kRowsIn;
-  constexpr int kSplit = split_rows(R, NG, kQ);
 
-  // kQ: the multipliers and shifts of this lane's four output channels, for
-  // every wave that walks rows, loaded before the walk (the MFMA waves
-  // first thing, the copy waves that walk rows once their copies are
-  // issued).  Channels past N read as zero (their values are never
+  // kQ: the multipliers and shifts of this lane's four output channels,
+  // loaded by the MFMA waves first thing (the walk needs them before its
+  // first row).  Channels past N read as zero (their values are never
   // stored).  Staged through LDS with the bias instead (16 active lanes per
   // copy wave) they measured 7.43-7.55 against 7.16-7.18 us per launch
   // (28x28x128, int8 output, same box).
   v4i qm{0, 0, 0, 0}, qs{0, 0, 0, 0};
-  auto load_q = [&]() {
-    if constexpr (kQ) {
+  if constexpr (kQ) {
+    if (!copier) {
       const int oc0 = tile_n + wave * 16 + 4 * (lane >> 4);
       const auto mr = make_rsrc(p.qmult, uint32_t(gemm_n) * 4u);
       const auto sr = make_rsrc(p.qshift, uint32_t(gemm_n) * 4u);
@@ -641,8 +634,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(
         qs[e] = __builtin_amdgcn_raw_buffer_load_b32(sr, uint32_t(oc0 + e) * 4u, 0, 0);
       }
     }
-  };
-  if (!copier) load_q();
+  }
 
   if (wave_id == 0 && lane < nchunks) {
     // every flag starts at zero before any copy can land
@@ -715,14 +707,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(
     else if (pw == 1) CopySchedule<R, 1, NG>::run(issue_chunk, signal);
     else CopySchedule<R, 2, NG>::run(issue_chunk, signal);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    // With a split, the copy wave then walks the block's last rows for its
-    // MFMA wave's 16 channels (its copies have landed; the chunk flags say
-    // when the other copy waves' have).
-    if constexpr (kSplit > 0) {
-      pin_sgprs(p);
-      load_q();
-      run_walk<R, NFR, NG, kQ, kSplit, R>(p, smem, wave, lane, b, oy0, rows_out, tile_n, qm, qs);
-    }
+    // the copy wave's work is done
     return;
   }
   // the remaining arguments, in one batch, while the first chunk lands
@@ -732,8 +717,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void rowpass_kernel(
   // us per launch at K = 20, same box.
   __builtin_amdgcn_s_setprio(3);
   flag_barrier();
-  run_walk<R, NFR, NG, kQ, 0, (kSplit > 0 ? kSplit : R)>(p, smem, wave, lane, b, oy0, rows_out,
-                                                          tile_n, qm, qs);
+  run_walk<R, NFR, NG, kQ, 0, R>(p, smem, wave, lane, b, oy0, rows_out, tile_n, qm, qs);
 }
 
 

@@ -80,9 +80,9 @@ ROWPASS_EDITS = [
      "      if (c == 0) { tl_put(p.tl, 31, tl_now()); tl_put(p.tl, 0, t_start); }\n"
      "      if (c == nchunks - 1) tl_put(p.tl, 2, tl_now());\n"
      "    };"),
-    ("    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n    // With a split",
+    ("    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n    // the copy wave's work is done",
      "    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n"
-     "    tl_put(p.tl, 3, tl_now());\n    // With a split"),
+     "    tl_put(p.tl, 3, tl_now());\n    // the copy wave's work is done"),
     ("  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n",
      "  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n"
      "  h.tl = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n) <= size_t(g_i8_timeline_wgs)\n"

@@ -73,9 +73,8 @@ EDGE = {
     "stream_nfr4": lab.ConvShape(16, 20, 60, 128, 64, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_nfr1": lab.ConvShape(8, 14, 14, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_pad0": lab.ConvShape(4, 30, 30, 128, 64, 3, 3, 0, 0, 1, 1, 1, 1),
-    # Blocks of 4-6 rows (in the requantizing form the copy waves walk
-    # their last rows): 4 rows with one fragment, 5/4 rows of 29 columns,
-    # 6/5 rows with a 96-channel tail (half a channel tile).
+    # Blocks of 4-6 rows: 4 rows with one fragment, 5/4 rows of 29
+    # columns, 6/5 rows with a 96-channel tail (half a channel tile).
     "stream_split_r4_nfr1": lab.ConvShape(32, 16, 16, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r5_w29": lab.ConvShape(32, 19, 29, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r6_k96": lab.ConvShape(32, 22, 13, 128, 96, 3, 3, 1, 1, 1, 1, 1, 1),

@@ -235,7 +235,7 @@ FUSED_EDGES = {
     "nfr4": lab.ConvShape(4, 20, 60, 128, 64, 3, 3, 1, 1, 1, 1, 1, 1),
     "r2_uneven": lab.ConvShape(8, 28, 28, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "pad0": lab.ConvShape(4, 30, 30, 128, 64, 3, 3, 0, 0, 1, 1, 1, 1),
-    # blocks whose last rows the copy waves walk (5/4 and 6/5 rows)
+    # blocks of 5/4 and 6/5 rows
     "split_r5_w29": lab.ConvShape(32, 19, 29, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "split_r6_k96": lab.ConvShape(32, 22, 13, 128, 96, 3, 3, 1, 1, 1, 1, 1, 1),
 }
