@@ -13,10 +13,16 @@ state), replayed from a HIP graph, ends in ~5 ms of replays the host does
 not wait for; the timed launches are enqueued behind them, so the GPU does
 not idle between the warmup and the timed launches.  The headline
 (ms_per_step) is the K steps as K back-to-back launches enqueued one by one
-on the stream between two HIP events (stream region), like the reference's
-launches (conv_lab.cu:88-110) but batched; the output is poisoned right
-before them and checked against the oracle after them.  Beside it, the same
-K launches as replays of a HIP graph of K launches (K <= 10000; larger K:
+on the stream (stream region), like the reference's launches
+(conv_lab.cu:88-110) but batched, timed by events that the launches
+themselves carry (hipExtLaunchKernel: the start of the first launch's first
+kernel to the end of the last launch's last kernel); the output is poisoned
+right before them and checked against the oracle after them.  The same
+launches between two HIP events recorded on the stream around them
+(config.event_bracketed_ms_per_step) also hold the two event packets'
+overhead, ~10 us on 28x28x128, which weighs on short runs (about 0.5 us
+per launch at K = 20; none at K = 2000, where both agree).  Beside it, the
+same K launches as replays of a HIP graph of K launches (K <= 10000; larger K:
 graphs of 10000 and a remainder) between events (config.graph_ms_per_step):
 each graph replay begins some microseconds after the previous one ends, a
 gap the graph region holds once per replay, which weighs on short runs
@@ -154,7 +160,7 @@ def write_floor(workload: str, steps: int, warmup: int, min_warmup_ms: float) ->
         t = lab.measure_store_floor(y, n, grid, 512, lds, through, warmup=warmup,
                                     min_warmup_ms=min_warmup_ms, iterations=steps,
                                     launches_per_graph=min(steps, 100))
-        us = t["mean_ms"] * 1e3
+        us = t["kernel_ms"] * 1e3  # timed like the headline
         out[f"{key}_us_per_launch"] = round(us, 3)
         if n:
             units = y.download(np.int32, n // 4).reshape(-1, 4)
@@ -335,7 +341,7 @@ def main() -> int:
     t = lab.measure_graph(kernel, shape, xb, wb, bb, yb, ws, ws_n, warmup=args.warmup,
                           min_warmup_ms=args.min_warmup_ms, iterations=args.steps,
                           launches_per_graph=per_graph, poison_byte=0xA5)
-    mean_ms = t["stream_ms"]
+    mean_ms = t["kernel_ms"]
     got = yb.download(np.int32, g.output_elements).reshape(shape.output_shape)
     if not np.array_equal(got, expected):
         print(f"bench.py: {kernel} output after the timed replays differs from the oracle",
@@ -381,11 +387,16 @@ def main() -> int:
             "ops_per_step": ops,
             "algorithmic_bytes_per_step": nbytes,
             "pct_int8_mfma_peak": round(100.0 * tops / PEAK_INT8_TOPS, 2),
-            "timing": f"{args.steps} back-to-back launches enqueued one by one on a stream "
-                      f"between two events, after {t['warmup_launches']} warmup launches over "
-                      f"{t['warmup_ms']:.0f} ms whose last ~5 ms the host does not wait for (the "
-                      f"timed launches are enqueued behind them: no idle GPU between warmup and "
-                      f"timing); output poisoned before and checked after the timed launches",
+            "timing": f"{args.steps} back-to-back launches enqueued one by one on a stream, "
+                      f"timed from the start of the first launch's kernel to the end of the last "
+                      f"one's by events the launches carry, after {t['warmup_launches']} warmup "
+                      f"launches over {t['warmup_ms']:.0f} ms whose last ~5 ms the host does not "
+                      f"wait for (the timed launches are enqueued behind them: no idle GPU between "
+                      f"warmup and timing); output poisoned before and checked after the timed "
+                      f"launches",
+            # the same launches between two events recorded on the stream
+            # around them (adds the event packets' overhead)
+            "event_bracketed_ms_per_step": round(t["stream_ms"], 6),
             "warmup_launches_run": t["warmup_launches"],
             "warmup_ms": round(t["warmup_ms"], 1),
             # the same K launches as graph replays, between events

@@ -284,6 +284,11 @@ typedef struct i8conv_graph_timing {
    * between one pair of events, after the poison fill that follows the
    * graph region: elapsed / iterations */
   float stream_ms;
+  /* the same K stream launches timed by events the launches themselves
+   * carry (hipExtLaunchKernel: the first kernel's start to the last
+   * kernel's end), without the two event packets around them:
+   * elapsed / iterations */
+  float kernel_ms;
 } i8conv_graph_timing;
 
 /* No counterpart in the reference, which times launches one by one

@@ -49,7 +49,7 @@ class CGraphTiming(ctypes.Structure):
     _fields_ = [("mean_ms", c_float), ("launches_per_graph", c_int), ("full_replays", c_int),
                 ("remainder_launches", c_int), ("warmup_launches", c_int),
                 ("warmup_ms", c_float), ("stamped_ms", c_float),
-                ("stream_ms", c_float)]
+                ("stream_ms", c_float), ("kernel_ms", c_float)]
 
 
 # name -> (restype, argtypes); every symbol include/i8conv.h declares.

@@ -131,6 +131,7 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   hipGraph_t graphs[4] = {nullptr, nullptr, nullptr, nullptr};
   hipGraphExec_t execs[4] = {nullptr, nullptr, nullptr, nullptr};
   hipEvent_t start = nullptr, stop = nullptr, sstart = nullptr, sstop = nullptr;
+  hipEvent_t kstart = nullptr, kstop = nullptr;
   // fills the output with the poison byte, enqueued on the stream (a fill
   // kernel outside any graph), so that a check after the stream region
   // sees only what its launches wrote
@@ -195,6 +196,8 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   if (rc == I8CONV_OK && (e = hipEventCreate(&start)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
   if (rc == I8CONV_OK && (e = hipEventCreate(&stop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
   if (rc == I8CONV_OK && (e = hipEventCreate(&sstart)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&kstart)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
+  if (rc == I8CONV_OK && (e = hipEventCreate(&kstop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
   if (rc == I8CONV_OK && (e = hipEventCreate(&sstop)) != hipSuccess) rc = hip_fail("hipEventCreate", e);
   if (rc == I8CONV_OK) rc = capture(0, per_graph);
   if (rc == I8CONV_OK && remainder > 0) rc = capture(1, remainder);
@@ -248,14 +251,27 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   // host, and the output then holds only what they wrote
   if (rc == I8CONV_OK) rc = poison();
   if (rc == I8CONV_OK && (e = hipEventRecord(sstart, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
-  for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) rc = launch(s);
+  // the first launch's first kernel also carries kstart, the last launch's
+  // kernels kstop: the launches timed by their own start and end
+  // timestamps, without the event packets around them
+  {
+    LaunchEvents &ev = launch_events();
+    ev.start = kstart;
+    for (int i = 0; i < iterations && rc == I8CONV_OK; ++i) {
+      if (i == iterations - 1) ev.stop = kstop;
+      rc = launch(s);
+    }
+    ev = LaunchEvents{};
+  }
   if (rc == I8CONV_OK && (e = hipEventRecord(sstop, s)) != hipSuccess) rc = hip_fail("hipEventRecord", e);
   if (rc == I8CONV_OK && (e = hipStreamSynchronize(s)) != hipSuccess) rc = hip_fail("hipStreamSynchronize", e);
-  float ms = 0.f, sms = 0.f;
+  float ms = 0.f, sms = 0.f, kms = 0.f;
   if (rc == I8CONV_OK && (e = hipEventElapsedTime(&ms, start, stop)) != hipSuccess)
     rc = hip_fail("hipEventElapsedTime", e);
   if (rc == I8CONV_OK && (e = hipEventElapsedTime(&sms, sstart, sstop)) != hipSuccess)
     rc = hip_fail("hipEventElapsedTime", e);
+  if (rc == I8CONV_OK && (e = hipEventElapsedTime(&kms, kstart, kstop)) != hipSuccess)
+    rc = hip_fail("hipEventElapsedTime(kernel events)", e);
   std::vector<unsigned long long> host(size_t(2 + 2 * stamp_cap), 0ull);
   if (rc == I8CONV_OK &&
       (e = hipMemcpy(host.data(), stamps, stamp_bytes, hipMemcpyDeviceToHost)) != hipSuccess)
@@ -275,6 +291,7 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
       timing->warmup_ms = float(warm_ms);
       timing->stamped_ms = float(double(t1s - t0s) / (double(rate_khz) * double(iterations)));
       timing->stream_ms = sms / float(iterations);
+      timing->kernel_ms = kms / float(iterations);
     }
   }
   // teardown: drain the stream first; a failure here cannot change the result
@@ -283,6 +300,8 @@ int measure_graph_loop(Launch launch, void *output, size_t out_bytes, int warmup
   if (start) (void)hipEventDestroy(start);
   if (stop) (void)hipEventDestroy(stop);
   if (sstart) (void)hipEventDestroy(sstart);
+  if (kstart) (void)hipEventDestroy(kstart);
+  if (kstop) (void)hipEventDestroy(kstop);
   if (sstop) (void)hipEventDestroy(sstop);
   for (int i = 0; i < 4; ++i) {
     if (execs[i]) (void)hipGraphExecDestroy(execs[i]);
@@ -341,6 +360,11 @@ constexpr int kDefaultSpinLimit = 1 << 20;
 std::atomic<int> g_spin_limit{kDefaultSpinLimit};
 }  // namespace
 int wait_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
+
+LaunchEvents &launch_events() {
+  static thread_local LaunchEvents events;
+  return events;
+}
 
 }  // namespace i8conv
 

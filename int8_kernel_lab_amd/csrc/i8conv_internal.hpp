@@ -9,6 +9,26 @@
 #include "i8conv.h"
 #include "i8conv_device.hpp"
 
+#ifdef __HIPCC__
+#include <hip/hip_ext.h>
+#endif
+
+#ifdef __HIPCC__
+// Launches a kernel on the lab's conv path; kernels launched while the
+// measurement loop has set launch_events() carry its events.
+#define I8_LAUNCH(kern, grid, block, lds, stream, ...)                                    \
+  do {                                                                                  \
+    ::i8conv::LaunchEvents &ev_ = ::i8conv::launch_events();                            \
+    if (ev_.start || ev_.stop) {                                                        \
+      hipExtLaunchKernelGGL(kern, grid, block, lds, stream, ev_.start, ev_.stop, 0,       \
+                            __VA_ARGS__);                                               \
+      ev_.start = nullptr;                                                              \
+    } else {                                                                            \
+      hipLaunchKernelGGL(kern, grid, block, lds, stream, __VA_ARGS__);                  \
+    }                                                                                   \
+  } while (0)
+#endif
+
 namespace i8conv {
 
 constexpr int kThreads = 256;      // 4 wave64 per workgroup
@@ -190,6 +210,17 @@ int rowpass_wait_expired(int *expired);
 // and the deep-channel split-K makes before it gives up; read at launch
 // (i8conv_set_wait_spin_limit; 2^20 by default)
 int wait_spin_limit();
+// capi.hip: events that the next kernel launches of this host thread carry
+// (hipExtLaunchKernel), set only by the measurement loop: `start` is taken
+// by the first kernel launched and cleared, `stop` by every kernel launched
+// while it is set (the last one's end stands).  Both null otherwise.
+#ifdef __HIPCC__
+struct LaunchEvents {
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
+};
+LaunchEvents &launch_events();
+#endif
 int launch_deepk(const ConvArgs &a, const DeepPlan &p, void *workspace, void *stream);
 int deepk_wait_expired(int *expired);
 // kernel_probe.hip: a store-only kernel (16-byte buffer stores, write-through

@@ -479,7 +479,7 @@ int launch_deepk(const ConvArgs &a, const DeepPlan &p, void *workspace, void *st
         return I8CONV_HIP_ERROR;
       }
     }
-    hipLaunchKernelGGL(kern, dim3(unsigned(grid)), dim3(2 * kThreads), p.lds, s, a.x, a.w,
+    I8_LAUNCH(kern, dim3(unsigned(grid)), dim3(2 * kThreads), p.lds, s, a.x, a.w,
                        uint32_t(a.c), uint32_t(a.gemm_n), uint32_t(a.n),
                        uint32_t(a.h) | uint32_t(a.wd) << 16,
                        uint32_t(a.pad_h) | uint32_t(a.pad_w) << 8, div_hw.mul,

@@ -283,10 +283,10 @@ template <int BM, int BN, int WM>
 int launch_tile(const ConvArgs &a, int splits, hipStream_t stream) {
   const int tiles = ((a.gemm_m + BM - 1) / BM) * ((a.gemm_n + BN - 1) / BN);
   if (splits > 1) {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, true>), dim3(tiles, splits),
+    I8_LAUNCH((gemm_kernel<BM, BN, WM, true>), dim3(tiles, splits),
                        dim3(kThreads), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, false>), dim3(tiles, 1),
+    I8_LAUNCH((gemm_kernel<BM, BN, WM, false>), dim3(tiles, 1),
                        dim3(kThreads), 0, stream, a);
   }
   const hipError_t e = hipGetLastError();
@@ -356,15 +356,15 @@ int launch_splitk(const ConvArgs &a, const GemmPlan &p, void *workspace,
   if (blocks > 4096) blocks = 4096;
   if (blocks == 0) blocks = 1;
   if (rq) {
-    hipLaunchKernelGGL(splitk_reduce_vec<true>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+    I8_LAUNCH(splitk_reduce_vec<true>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
                        args.partial, a.bias, nullptr, a.gemm_n / 4, total / 4, p.splits, rq->mult,
                        rq->shift, rq->zero_point, reinterpret_cast<uint32_t *>(rq->y));
   } else if (vec) {
-    hipLaunchKernelGGL(splitk_reduce_vec<false>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+    I8_LAUNCH(splitk_reduce_vec<false>, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
                        args.partial, a.bias, a.y, a.gemm_n / 4, total / 4, p.splits, nullptr,
                        nullptr, 0, nullptr);
   } else {
-    hipLaunchKernelGGL(splitk_reduce_scalar, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
+    I8_LAUNCH(splitk_reduce_scalar, dim3(unsigned(blocks)), dim3(kThreads), 0, s,
                        args.partial, a.bias, a.y, a.gemm_n, total, p.splits);
   }
   const hipError_t e = hipGetLastError();

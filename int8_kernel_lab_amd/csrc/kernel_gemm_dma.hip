@@ -406,7 +406,7 @@ int launch_tile(const ConvArgs &a, int splits, hipStream_t stream) {
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(tiles), unsigned(splits)), dim3(64 * (WM * WN + NCW)),
+  I8_LAUNCH(kern, dim3(unsigned(tiles), unsigned(splits)), dim3(64 * (WM * WN + NCW)),
                      lds, stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -263,7 +263,7 @@ int launch_t(const ConvArgs &a, const HaloArgs &h, size_t blocks, size_t lds, hi
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(kThreads), lds, s, a, h);
+  I8_LAUNCH(kern, dim3(unsigned(blocks)), dim3(kThreads), lds, s, a, h);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error(std::string("halo kernel launch: ") + hipGetErrorString(e));

@@ -236,7 +236,7 @@ int launch_t(const ConvArgs &a, const PatchArgs &pa, size_t blocks, size_t lds,
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(kThreads), lds, s, a, pa);
+  I8_LAUNCH(kern, dim3(unsigned(blocks)), dim3(kThreads), lds, s, a, pa);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error(std::string("patch kernel launch: ") + hipGetErrorString(e));

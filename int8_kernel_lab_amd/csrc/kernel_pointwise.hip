@@ -261,11 +261,11 @@ int launch_pw(const ConvArgs &a, const RequantArgs *rq, hipStream_t stream) {
     constexpr int kD = KS >= 4 ? 2 : 8 / KS;
     if constexpr (NA % 4 == 0 && NA <= 8) {
       if (int64_t(a.gemm_m) * a.gemm_n > kStreamOutputBytes)
-        hipLaunchKernelGGL((pointwise_kernel<NA, KS, SL, kD, kBig, true>), grid, block,
+        I8_LAUNCH((pointwise_kernel<NA, KS, SL, kD, kBig, true>), grid, block,
                            0, stream, a.x, a.w, a.bias, nullptr, a.gemm_m, nfrag, rq->mult,
                            rq->shift, rq->zero_point, rq->y);
       else
-        hipLaunchKernelGGL((pointwise_kernel<NA, KS, SL, kD, kSmall, true>), grid,
+        I8_LAUNCH((pointwise_kernel<NA, KS, SL, kD, kSmall, true>), grid,
                            block, 0, stream, a.x, a.w, a.bias, nullptr, a.gemm_m, nfrag, rq->mult,
                            rq->shift, rq->zero_point, rq->y);
     } else {
@@ -274,11 +274,11 @@ int launch_pw(const ConvArgs &a, const RequantArgs *rq, hipStream_t stream) {
       return I8CONV_BAD_ARGUMENT;
     }
   } else if (int64_t(a.gemm_m) * a.gemm_n * 4 > kStreamOutputBytes) {
-    hipLaunchKernelGGL((pointwise_kernel<NA, KS, SL, pw_depth(KS), kStoreStream, false>), grid,
+    I8_LAUNCH((pointwise_kernel<NA, KS, SL, pw_depth(KS), kStoreStream, false>), grid,
                        block, 0, stream, a.x, a.w, a.bias, a.y, a.gemm_m, nfrag, nullptr, nullptr,
                        0, nullptr);
   } else {
-    hipLaunchKernelGGL((pointwise_kernel<NA, KS, SL, pw_depth(KS), kStoreThrough, false>), grid,
+    I8_LAUNCH((pointwise_kernel<NA, KS, SL, pw_depth(KS), kStoreThrough, false>), grid,
                        block, 0, stream, a.x, a.w, a.bias, a.y, a.gemm_m, nfrag, nullptr, nullptr,
                        0, nullptr);
   }

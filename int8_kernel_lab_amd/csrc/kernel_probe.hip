@@ -65,7 +65,7 @@ int launch_t(int32_t *y, uint32_t units, int workgroups, int threads, size_t lds
     }
   }
   const uint32_t slice = (units + uint32_t(workgroups) - 1) / uint32_t(workgroups);
-  hipLaunchKernelGGL(kern, dim3(unsigned(workgroups)), dim3(unsigned(threads)), lds, s, y, units,
+  I8_LAUNCH(kern, dim3(unsigned(workgroups)), dim3(unsigned(threads)), lds, s, y, units,
                      slice);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -128,7 +128,7 @@ int launch_lds_t(int32_t *sink, int workgroups, int threads, int iters, hipStrea
     set_error(std::string("hipFuncSetAttribute: ") + hipGetErrorString(a));
     return I8CONV_HIP_ERROR;
   }
-  hipLaunchKernelGGL(kern, dim3(unsigned(workgroups)), dim3(unsigned(threads)), kProbeLds, s,
+  I8_LAUNCH(kern, dim3(unsigned(workgroups)), dim3(unsigned(threads)), kProbeLds, s,
                      sink, iters);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -65,10 +65,10 @@ int launch_requant(const int32_t *acc, int64_t pixels, int32_t channels, const i
   // the kernels only repeats for tensors beyond 2^28 items
   const unsigned blocks = unsigned(std::min<size_t>((items + kThreads - 1) / kThreads, 1u << 20));
   if (vec)
-    hipLaunchKernelGGL(requant_vec, dim3(blocks), dim3(kThreads), 0, s, acc, mult, shift,
+    I8_LAUNCH(requant_vec, dim3(blocks), dim3(kThreads), 0, s, acc, mult, shift,
                        zero_point, reinterpret_cast<uint32_t *>(out), channels / 4, items);
   else
-    hipLaunchKernelGGL(requant_scalar, dim3(blocks), dim3(kThreads), 0, s, acc, mult, shift,
+    I8_LAUNCH(requant_scalar, dim3(blocks), dim3(kThreads), 0, s, acc, mult, shift,
                        zero_point, out, channels, total);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

@@ -380,7 +380,7 @@ int launch_t(const RowPre &a, const RowArgs &h, dim3 grid, size_t lds, hipStream
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), lds, s, a.x, a.w, a.bias, a.n, a.hw, a.pads,
+  I8_LAUNCH(kern, grid, dim3(kThreads), lds, s, a.x, a.w, a.bias, a.n, a.hw, a.pads,
                      a.gemm_n, a.ring, h);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {

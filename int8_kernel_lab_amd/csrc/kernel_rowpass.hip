@@ -741,7 +741,7 @@ int launch_q(const PreArgs &a, const PassArgs &h, dim3 grid, size_t lds, hipStre
       return I8CONV_HIP_ERROR;
     }
   }
-  hipLaunchKernelGGL(kern, grid, dim3(2 * kThreads), lds, s, a.x, a.w, a.bias, a.n, a.hw, a.pads,
+  I8_LAUNCH(kern, grid, dim3(2 * kThreads), lds, s, a.x, a.w, a.bias, a.n, a.hw, a.pads,
                      a.gemm_n, h);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
