@@ -169,12 +169,8 @@ struct RequantOdd {
 };
 I8_HD inline RequantOdd requant_odd_params(int32_t mult, int32_t shift, int32_t zp) {
   const int s = shift < 0 ? 0 : (shift > 62 ? 62 : shift);
-  int t = 0;
-  uint32_t m = uint32_t(mult);
-  while (m != 0 && (m & 1u) == 0) {
-    m >>= 1;
-    ++t;
-  }
+  // trailing zeros (a uniform mult gives one s_ff1 on the device)
+  const int t = mult == 0 ? 0 : __builtin_ctz(uint32_t(mult));
   RequantOdd r;
   r.mo = mult == 0 ? 0 : int32_t(int64_t(mult) >> t);
   const int sh = mult == 0 ? 1 : s - t - 32;
@@ -186,7 +182,14 @@ I8_HD inline RequantOdd requant_odd_params(int32_t mult, int32_t shift, int32_t 
   return r;
 }
 I8_HD inline int32_t requant1_odd(int32_t acc, int32_t mo, int32_t k, int32_t sh) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // one v_mul_hi_i32: written as a 64-bit product, the compiler made it a
+  // full 64 x 64 multiply (three quarter-rate operations) where it could
+  // not see that mo is a sign-extended 32-bit value
+  const int32_t hi = __mulhi(acc, mo);
+#else
   const int32_t hi = int32_t((int64_t(acc) * int64_t(mo)) >> 32);
+#endif
   const int32_t v = (hi + k) >> sh;
   return v < -128 ? -128 : (v > 127 ? 127 : v);
 }
