@@ -319,9 +319,12 @@ typedef struct i8conv_graph_timing {
  *   7. when poison_byte >= 0, the output is filled with that byte (a fill on
  *      the stream, outside any graph); then the stream region: the K
  *      launches enqueued one by one on the stream (no graph) between one
- *      pair of events (stream_ms).  They are enqueued while the tail still
- *      runs, so the GPU does not wait for the host, and the output then
- *      holds only what they wrote.
+ *      pair of events (stream_ms).  The first of them also carries a start
+ *      event and the last a stop event of its own (hipExtLaunchKernel),
+ *      whose interval, from the first kernel's start to the last one's end,
+ *      gives kernel_ms.  They are enqueued while the tail still runs, so the
+ *      GPU does not wait for the host, and the output then holds only what
+ *      they wrote.
  * Fills *timing.  Synchronous. */
 int i8conv_measure_graph(int id, const i8conv_shape *shape, const int8_t *input,
                          const int8_t *filter, const int32_t *bias, int32_t *output,
