@@ -116,11 +116,14 @@ __global__ __launch_bounds__(64 * pw_group_waves(SL)) void pointwise_kernel(
   v4i b4[NA];
 #pragma unroll
   for (int a = 0; a < NA; ++a) b4[a] = load16(br, (oc0 + uint32_t(16 * a + 4 * g)) * 4u);
-  v4i m4[RQ ? NA : 1], s4[RQ ? NA : 1];
-  // short form (requant1_short) when every channel of the wave's slice has
-  // shift >= 33 and |zp| <= 2^30: a uniform choice per wave; m4 and s4 then
-  // hold am and shx (pw_requant4_short)
-  bool qshort = false;
+  v4i m4[RQ ? NA : 1], s4[RQ ? NA : 1], h4[RQ ? NA : 1];
+  // The requantization's form, a uniform choice per wave: the odd-
+  // multiplier form (requant4_odd: m4, s4 and h4 then hold mo, k and sh)
+  // when every channel of the wave's slice is in its domain, four VALU
+  // operations per value; else the short form (requant1_short) when every
+  // channel has shift >= 33 and |zp| <= 2^30 (m4 and s4 then hold am and
+  // shx: pw_requant4_short), about a dozen; else the exact form (requant4).
+  bool qodd = false, qshort = false;
   if constexpr (RQ) {
     const auto mr = make_rsrc(mult, kN * 4u), sr = make_rsrc(shift, kN * 4u);
 #pragma unroll
@@ -128,7 +131,27 @@ __global__ __launch_bounds__(64 * pw_group_waves(SL)) void pointwise_kernel(
       m4[a] = load16(mr, (oc0 + uint32_t(16 * a + 4 * g)) * 4u);
       s4[a] = load16(sr, (oc0 + uint32_t(16 * a + 4 * g)) * 4u);
     }
-    bool ok = requant_short_zp_ok(zp);
+    v4i mo4[NA], k4[NA];
+    bool okodd = true;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const RequantOdd o = requant_odd_params(m4[a][e], s4[a][e], zp);
+        okodd = okodd && o.ok;
+        mo4[a][e] = o.mo;
+        k4[a][e] = o.k;
+        h4[a][e] = o.sh;
+      }
+    qodd = __builtin_amdgcn_ballot_w64(!okodd) == 0;
+    if (qodd) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        m4[a] = mo4[a];
+        s4[a] = k4[a];
+      }
+    }
+    bool ok = !qodd && requant_short_zp_ok(zp);
 #pragma unroll
     for (int a = 0; a < NA; ++a)
 #pragma unroll
@@ -178,7 +201,11 @@ __global__ __launch_bounds__(64 * pw_group_waves(SL)) void pointwise_kernel(
 #pragma unroll
         for (int h = 0; h < kGroups; ++h) {
           uint32_t dq[4];
-          if (qshort) {
+          if (qodd) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+              dq[a] = requant4_odd(acc[4 * h + a], m4[4 * h + a], s4[4 * h + a], h4[4 * h + a]);
+          } else if (qshort) {
 #pragma unroll
             for (int a = 0; a < 4; ++a)
               dq[a] = pw_requant4_short(acc[4 * h + a], m4[4 * h + a], s4[4 * h + a], zp);

@@ -358,6 +358,34 @@ def test_pointwise_requant_short_form_bit_exact(name, mixed):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("name", ["c64_k64_tail", "c128_k256_slices2", "c256_k256_slices4",
+                                  "c64_k128"])
+@pytest.mark.parametrize("mixed", [False, True])
+def test_pointwise_requant_odd_form_bit_exact(name, mixed):
+    # multipliers of both signs with 0..8 trailing zeros and shifts raised to
+    # match: every wave takes the odd-multiplier form, whose normalization
+    # (mult = mo 2^t, s' = s - t) decides every value; mixed: one channel of
+    # the last slice with s' = 32 (outside the odd form, inside the short
+    # one) sends that slice's waves to the short form
+    from tests.conftest import say
+    shape = POINTWISE_RQ[name]
+    x, w, b = lab.make_case_data(shape, seed=17)
+    rng = np.random.default_rng(18)
+    t = rng.integers(0, 9, size=shape.k)
+    mult = ((rng.integers(2 ** 22, 2 ** 23, size=shape.k) * 2 + 1)
+            * rng.choice([-1, 1], size=shape.k) << t).astype(np.int32)
+    shift = (rng.integers(35, 38, size=shape.k) + t).astype(np.int32)
+    if mixed:
+        mult[shape.k - 3] = 3 << 4
+        shift[shape.k - 3] = 36
+    say(f"[gpu] pointwise requant odd form {name} mixed={mixed}")
+    got = lab.conv2d_requant(x, w, b, mult, shift, 7, shape)
+    exp = oracle.requantize(oracle.conv(shape, x, w, b), mult, shift, 7)
+    assert len(np.unique(exp)) > 200
+    np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.gpu
 def test_pointwise_requant_unaligned_output_takes_the_unfused_path():
     # output at +4 bytes: the convolution into the int32 workspace and the
     # requantizing pass, bit-exact, nothing written outside the output
