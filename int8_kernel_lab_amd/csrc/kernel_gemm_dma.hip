@@ -362,7 +362,14 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
   };
   // Requantized int8 output: a lane's four channels of a pixel as one
   // 4-byte store (a pixel's 16-channel slice, 16 bytes, per four lanes;
-  // ordinary stores, merged into lines in the L2).
+  // ordinary stores, merged into lines in the L2).  Per 16-channel fragment
+  // row, the odd-multiplier form (requant4_odd: four VALU operations per
+  // value) where every channel of the wave's fragment row is in its domain
+  // (a ballot over the active lanes), else the exact form (requant4, three
+  // quarter-rate multiplies per value).  With int8 output, same box: the
+  // 3x3 stride-2 128 -> 256-channel layer (config 3) 16.67-16.74 -> 15.73-
+  // 15.76 us per launch, the dilated 256-channel one (config 5b) 25.64-25.69
+  // -> 24.53-24.64.
   auto store_tile_requant = [&]() {
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
@@ -370,12 +377,32 @@ __global__ __launch_bounds__(64 * (WM * WN + NCW)) void gemm_dma_kernel(ConvArgs
       if (oc0 >= a.gemm_n) continue;
       const v4i m = *reinterpret_cast<const v4i *>(a.q_mult + oc0);
       const v4i sh = *reinterpret_cast<const v4i *>(a.q_shift + oc0);
+      v4i mo, k, h;
+      bool ok = true;
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
-        if (px >= m_end) continue;
-        *reinterpret_cast<uint32_t *>(a.q_y + size_t(px) * size_t(a.gemm_n) + oc0) =
-            requant4(add_wrap(acc[i][j], bias[i]), m, sh, a.q_zp);
+      for (int e = 0; e < 4; ++e) {
+        const RequantOdd o = requant_odd_params(m[e], sh[e], a.q_zp);
+        ok = ok && o.ok;
+        mo[e] = o.mo;
+        k[e] = o.k;
+        h[e] = o.sh;
+      }
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0) {
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
+          if (px >= m_end) continue;
+          *reinterpret_cast<uint32_t *>(a.q_y + size_t(px) * size_t(a.gemm_n) + oc0) =
+              requant4_odd(add_wrap(acc[i][j], bias[i]), mo, k, h);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int px = tile_m + wm * TMW + j * 16 + (lane & 15);
+          if (px >= m_end) continue;
+          *reinterpret_cast<uint32_t *>(a.q_y + size_t(px) * size_t(a.gemm_n) + oc0) =
+              requant4(add_wrap(acc[i][j], bias[i]), m, sh, a.q_zp);
+        }
       }
     }
   };
