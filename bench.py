@@ -141,10 +141,9 @@ def write_floor(workload: str, steps: int, warmup: int, min_warmup_ms: float) ->
     store-only kernel (i8conv_measure_store_floor) writing exactly the
     layer's int32 output bytes with the row kernel's 16-byte write-through
     stores, in its launch shape (workgroups x 512 threads, the same dynamic
-    LDS), timed as graph replays between events (the headline's
-    graph_ms_per_step method: a short kernel's stream launches can be
-    host-bound); beside it, an empty kernel of the same shape (the dispatch
-    floor) and ordinary stores."""
+    LDS), timed like the headline (stream launches timed by the events the
+    first and last of them carry); beside it, an empty kernel of the same
+    shape (the dispatch floor) and ordinary stores."""
     import numpy as np
     import int8_kernel_lab_amd as lab
     shape = lab.load_case(os.path.join(lab.WORKLOADS_DIR, "baseline.csv"), workload)
@@ -203,6 +202,49 @@ def lds_probe(steps: int, warmup: int, min_warmup_ms: float) -> int:
             out["bytes_per_launch"] / (us * 1e-6) / 256 / 2.4e9, 1)
     sink.close()
     print(json.dumps(out), flush=True)
+    return 0
+
+
+def dispatch_floor(steps: int, warmup: int, min_warmup_ms: float) -> int:
+    """The dispatch floor over launch shapes: an empty kernel (the lab's
+    store-only kernel with nothing to store, i8conv_measure_store_floor) in
+    64, 256, 512 and 768 threads per workgroup x 128, 256, 512 and 1024
+    workgroups, with no dynamic LDS and with 160 KB, and beside each
+    (threads, workgroups) pair the same kernel writing config 2's 12.85 MB
+    int32 output with 16-byte write-through stores; every figure timed like
+    the headline.  One JSON line."""
+    import numpy as np
+    import int8_kernel_lab_amd as lab
+    nbytes = 12845056
+    y = lab.DeviceBuffer(nbytes)
+    rows = []
+
+    def timed(n, wg, threads, lds):
+        t = lab.measure_store_floor(y, n, wg, threads, lds, True, warmup=warmup,
+                                    min_warmup_ms=min_warmup_ms, iterations=steps,
+                                    launches_per_graph=min(steps, 100))
+        return round(t["kernel_ms"] * 1e3, 3)
+
+    try:
+        for threads in (64, 256, 512, 768):
+            for wg in (128, 256, 512, 1024):
+                row = {"threads": threads, "workgroups": wg,
+                       "empty_us": timed(0, wg, threads, 0),
+                       "empty_160kb_lds_us": timed(0, wg, threads, 160 * 1024),
+                       "write_12_85mb_us": timed(nbytes, wg, threads, 0)}
+                units = y.download(np.int32, nbytes // 4).reshape(-1, 4)
+                if not (units == np.arange(units.shape[0], dtype=np.int32)[:, None]).all():
+                    print("bench.py: the store floor kernel left wrong bytes", file=sys.stderr)
+                    return 1
+                rows.append(row)
+    finally:
+        y.close()
+    empty = [r[k] for r in rows for k in ("empty_us", "empty_160kb_lds_us")]
+    extra = [r["write_12_85mb_us"] - r["empty_us"] for r in rows]
+    print(json.dumps({"dispatch_floor": rows, "launches": steps,
+                      "empty_us_min": min(empty), "empty_us_max": max(empty),
+                      "write_minus_empty_us_min": round(min(extra), 3),
+                      "write_minus_empty_us_max": round(max(extra), 3)}), flush=True)
     return 0
 
 
@@ -287,6 +329,9 @@ def main() -> int:
                     help="instead of the benchmark, time the lab's store-only kernel writing "
                          "exactly the workload's int32 output bytes in the dispatched row "
                          "kernel's launch shape (and an empty kernel of that shape)")
+    ap.add_argument("--dispatch-floor", action="store_true",
+                    help="instead of the benchmark, time an empty kernel (and one writing "
+                         "config 2's output) over a grid of launch shapes")
     ap.add_argument("--lds-probe", action="store_true",
                     help="instead of the benchmark, time the LDS read probe in its four "
                          "patterns (the control for the LDS bank-conflict counters)")
@@ -309,6 +354,8 @@ def main() -> int:
         return lds_probe(args.steps, args.warmup, args.min_warmup_ms)
     if args.write_floor:
         return write_floor(args.workload, args.steps, args.warmup, args.min_warmup_ms)
+    if args.dispatch_floor:
+        return dispatch_floor(args.steps, args.warmup, args.min_warmup_ms)
 
     import numpy as np
     import int8_kernel_lab_amd as lab
