@@ -247,7 +247,9 @@ __global__ __launch_bounds__(kThreads, 1) void row_kernel(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int n = int(n_pre);
+  // bit 31 of n_pre: the grid groups images by XCD (below)
+  const bool by_xcd = (n_pre >> 31) != 0;
+  const int n = int(n_pre & 0xffffu);
   const int h = int(hw_pre & 0xffffu), wd = int(hw_pre >> 16);
   const int pad_h = int(pads_pre & 0xffu), pad_w = int((pads_pre >> 8) & 0xffu);
   const int blocks = int(pads_pre >> 16);
@@ -261,9 +263,14 @@ __global__ __launch_bounds__(kThreads, 1) void row_kernel(
   const int row_copies = (row_units + 63) >> 6;
   const int row_bytes = 16 * (64 * row_copies + (((row_units - 64 * row_copies) % 16) + 16) % 16);
 
-  const int tn = int(blockIdx.x);
+  // grid: (channel tiles, row blocks, images), or with by_xcd (n % 8 == 0)
+  // (8 x channel tiles, row blocks, images / 8) with blockIdx.x = x + 8 tn
+  // and image 8 blockIdx.z + x: workgroup i of a launch runs on XCD i mod 8
+  // = x, so every workgroup of an image runs on one XCD, whose L2 fetches
+  // the image's rows from HBM once for all of them.
+  const int tn = by_xcd ? int(blockIdx.x >> 3) : int(blockIdx.x);
   const int q = int(blockIdx.y);
-  const int b = int(blockIdx.z);
+  const int b = by_xcd ? int(8 * blockIdx.z + (blockIdx.x & 7)) : int(blockIdx.z);
   // out_h < 2^16 and q < blocks <= out_h: the products fit in 32 bits
   const int oy0 = int(uint32_t(q * out_h) / uint32_t(blocks));
   const int rows_out = int(uint32_t((q + 1) * out_h) / uint32_t(blocks)) - oy0;
@@ -437,7 +444,9 @@ int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream) {
   pre.x = a.x;
   pre.w = a.w;
   pre.bias = a.bias;
-  pre.n = uint32_t(a.n);
+  // n % 8 == 0: the grid groups each image's workgroups on one XCD
+  const bool by_xcd = a.n % 8 == 0;
+  pre.n = uint32_t(a.n) | (by_xcd ? 0x80000000u : 0u);
   pre.hw = uint32_t(a.h) | uint32_t(a.wd) << 16;
   pre.pads = uint32_t(a.pad_h) | uint32_t(a.pad_w) << 8 | uint32_t(p.ranges) << 16;
   pre.gemm_n = uint32_t(a.gemm_n);
@@ -449,7 +458,8 @@ int launch_row(const ConvArgs &a, const PatchPlan &p, void *stream) {
   h.out_w = a.out_w;
   h.gemm_n = a.gemm_n;
   h.row_bytes = int(row.row_bytes);
-  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));
+  const dim3 grid = by_xcd ? dim3(8 * unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n / 8))
+                           : dim3(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define I8_ROW_CASE(FN, CG, NFR) \
   if (fn == FN && cg == CG && nfr == NFR) return launch_t<FN, CG, NFR>(pre, h, grid, lds, s);

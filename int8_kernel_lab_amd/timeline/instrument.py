@@ -83,8 +83,8 @@ ROWPASS_EDITS = [
     ("    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n    // the copy wave's work is done",
      "    asm volatile(\"s_waitcnt lgkmcnt(0)\" ::: \"memory\");\n"
      "    tl_put(p.tl, 3, tl_now());\n    // the copy wave's work is done"),
-    ("  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n",
-     "  const dim3 grid(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n"
+    ("                           : dim3(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n",
+     "                           : dim3(unsigned(p.tiles_n), unsigned(p.ranges), unsigned(a.n));\n"
      "  h.tl = size_t(a.n) * size_t(p.ranges) * size_t(p.tiles_n) <= size_t(g_i8_timeline_wgs)\n"
      "             ? g_i8_timeline : nullptr;\n"),
     ("namespace i8conv {\n\n// Set by a wave of rowpass_kernel",

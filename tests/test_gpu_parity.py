@@ -78,6 +78,13 @@ EDGE = {
     "stream_split_r4_nfr1": lab.ConvShape(32, 16, 16, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r5_w29": lab.ConvShape(32, 19, 29, 128, 128, 3, 3, 1, 1, 1, 1, 1, 1),
     "stream_split_r6_k96": lab.ConvShape(32, 22, 13, 128, 96, 3, 3, 1, 1, 1, 1, 1, 1),
+    # n % 8 == 0 launches the row kernels on the grid that keeps each image
+    # on one XCD (blockIdx.x = image % 8 + 8 x channel tile): four channel
+    # tiles with a partial last one (copy-wave kernel and the c = 64 one),
+    # and three groups of eight images with a 36-channel tile.
+    "stream_xcd_k200": lab.ConvShape(8, 14, 14, 128, 200, 3, 3, 1, 1, 1, 1, 1, 1),
+    "row_xcd_k200": lab.ConvShape(8, 28, 28, 64, 200, 3, 3, 1, 1, 1, 1, 1, 1),
+    "row_xcd_n24_k36": lab.ConvShape(24, 14, 14, 64, 36, 3, 3, 1, 1, 1, 1, 1, 1),
     # c == 128 3x3 stride 2 (config 3's family): a 4-channel tail in the
     # second 128-channel tile; no padding with odd input sizes and 64
     # channels; 20-column output rows with a 72-channel tail.
