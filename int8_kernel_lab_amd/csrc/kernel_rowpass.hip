@@ -178,6 +178,30 @@ struct PassState {
   // its last chunk's
   static constexpr int kDecide = 4;
 
+  // The requantizing two-group full-store walk's MFMA order within a step:
+  // the row that the step completes (fy = 2) first, interleaved with the
+  // fy = 1 row, then fy = 0 with the rest of fy = 1 (entries: fy, block
+  // g * 3 + fx; each entry is NFR MFMAs), so that at least four accumulator
+  // chains alternate; the completed row is requantized and stored in the
+  // same step, six MFMAs after its last, one step earlier than the order
+  // below allows, and the walk's last row in its last step.  28x28x128 with
+  // int8 output: 6.52-6.57 -> 6.19-6.21 us per launch (same box); with int32
+  // output the same order measured 4.84 -> 4.87 us, so that walk keeps the
+  // (g, fx, fy) order and stores each row in the step after.
+  static constexpr int kOrderFy[18] = {2, 2, 1, 2, 2, 1, 2, 2, 1, 0, 0, 1, 0, 0, 1, 0, 0, 1};
+  static constexpr int kOrderB[18] = {0, 1, 0, 2, 3, 1, 4, 5, 2, 0, 1, 3, 2, 3, 4, 4, 5, 5};
+  // index of the MFMA after which row ir - 2's stores go: six after its last
+  static constexpr int early_sa(int ir) {
+    int n = 0, done = 0;
+    for (int e = 0; e < 18; ++e) {
+      const int o = ir - kOrderFy[e];
+      if (o >= OLO && o < OHI) {
+        n += NFR;
+        if (kOrderFy[e] == 2) done = n;
+      }
+    }
+    return done + 5 < n - 1 ? done + 5 : n - 1;
+  }
   static constexpr int mfmas_in_step(int ir) {
     int n = 0;
     for (int fy = 0; fy < 3; ++fy) n += (ir - fy >= OLO && ir - fy < OHI) ? 1 : 0;
@@ -248,7 +272,9 @@ struct PassState {
     // that completed it have drained.
     // Otherwise (a branch per row: element stores, or a block with fewer
     // rows than the walk) it is stored first thing.
-    constexpr bool kStoreHere = G + NG == kGroups && IR >= OLO + 3;
+    constexpr bool kEarly = kMode == kStoreFull && NG == 2 && kQ;
+    constexpr bool kEarlyHere = kEarly && G + NG == kGroups && IR - 2 >= OLO && IR - 2 < OHI;
+    constexpr bool kStoreHere = !kEarly && G + NG == kGroups && IR >= OLO + 3;
     constexpr bool kInStep = kStoreHere && kMode == kStoreFull;
     if constexpr (kStoreHere && !kInStep)
       store_row<IR - 3>(p, kMode != kStoreElem, rows_out, m_row0, oc0, lane);
@@ -277,6 +303,18 @@ struct PassState {
       if (fy_next <= 2) take_taps<G, (fy_next <= 2 ? fy_next : 0)>(lane);
       load_row<G>(p, IR + 1);
     }
+    if constexpr (kEarly) {
+#pragma unroll
+      for (int e = 0; e < 18; ++e) {
+        const int fy = kOrderFy[e], bb = kOrderB[e], g = bb / 3, fx = bb % 3;
+        const int o = IR - fy;
+        if (o >= OLO && o < OHI) {
+#pragma unroll
+          for (int j = 0; j < NFR; ++j)
+            acc[o][j] = mfma16(wf[g][fy * 3 + fx], cur[g][fx][j], acc[o][j]);
+        }
+      }
+    } else {
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
 #pragma unroll
@@ -291,6 +329,18 @@ struct PassState {
           }
         }
       }
+    }
+    }
+    if constexpr (kEarlyHere && kQ) {
+#pragma unroll
+      for (int j = 0; j < NFR; ++j)
+        __builtin_amdgcn_raw_buffer_store_b32(requant4_odd(acc[IR - 2][j], qmo, qk, qsh), yr,
+                                              voff[j], (IR - 2) * row_stride, 0);
+    } else if constexpr (kEarlyHere) {
+#pragma unroll
+      for (int j = 0; j < NFR; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(acc[IR - 2][j], yr, voff[j],
+                                               (IR - 2) * row_stride, kStoreThrough);
     }
     if constexpr (kInStep && kQ) {
       // kStoreFull with kQ: the wave takes the odd-multiplier form (qodd),
@@ -309,7 +359,8 @@ struct PassState {
     // the next row's reads go between this row's MFMAs (issued all ahead of
     // them, they held the MFMAs back: 6.7 -> 6.5 us per launch on 28x28x128)
     constexpr int kNM = mfmas_in_step(IR);
-    interleave<reads_in_step(IR), kNM, (kNM < 6 ? kNM - 1 : 5), (kInStep ? NFR : 0)>(
+    interleave<reads_in_step(IR), kNM, (kEarlyHere ? early_sa(IR) : (kNM < 6 ? kNM - 1 : 5)),
+               ((kInStep || kEarlyHere) ? NFR : 0)>(
         std::make_index_sequence<kNM>{});
   }
 
@@ -544,7 +595,8 @@ __device__ __forceinline__ void run_walk(const PassArgs &p, const int8_t *smem, 
     constexpr int M = decltype(mode)::value;
     st.template walk<0, M>(p, rows_out, m_row0, oc0, lane);
     if constexpr (NG == 1) st.template walk<1, M>(p, rows_out, m_row0, oc0, lane);
-    st.template store_row<OHI - 1>(p, M != kStoreElem, rows_out, m_row0, oc0, lane);
+    if constexpr (!(M == kStoreFull && NG == 2 && kQ))
+      st.template store_row<OHI - 1>(p, M != kStoreElem, rows_out, m_row0, oc0, lane);
   };
   if (vec && rows_out >= OHI && (!kQ || st.qodd))
     walks(std::integral_constant<int, kStoreFull>{});
